@@ -1,0 +1,57 @@
+"""Build the in-tree HIP library ``lib/libcgdr_fwd_h.so`` for gfx950.
+
+``python -m cgdr_amd.build`` (with ``cann-operator-challenge-august_amd`` on sys.path), or
+``build_library()`` from Python.  hipcc cross-compiles without a GPU.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+REPO_ROOT = os.path.dirname(_PKG_ROOT)
+CSRC = os.path.join(_PKG_ROOT, "csrc")
+LIB_DIR = os.path.join(_PKG_ROOT, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libcgdr_fwd_h.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 in device code.
+# -amdgpu-mfma-vgpr-form: MFMA accumulators in VGPRs, so the state is not shuttled between
+# AGPRs and VGPRs around every chunk's VALU work.
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
+    "-Wall", "-Wno-unused-function",
+    # The direct-to-LDS DMA asm clobbers M0; no other code in these kernels uses M0
+    # (checked on the generated assembly), so the reserved-register warning is noise.
+    "-Wno-inline-asm",
+]
+
+SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip")]
+HEADERS = [os.path.join(CSRC, "cgdr_kernels.h"), os.path.join(REPO_ROOT, "include", "cgdr_fwd_h.h")]
+
+
+def build_library(verbose: bool = False) -> str:
+    """Compile the library (always, even if a built copy exists) and return its path."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, *SOURCES, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

@@ -1,0 +1,405 @@
+// cgdr_fwd_h.hip -- C ABI of the gfx950 ChunkGatedDeltaRuleFwdH operator (include/cgdr_fwd_h.h).
+//
+// Host side: argument validation (the role of InferShapeChunkGatedDeltaRuleFwdH,
+// code/op_host/chunk_gated_delta_rule_fwd_h_infershape.cpp:135-298 of the reference, without
+// its Ascend-only limits B=1, K==V and N<=4), the launch plan (the role of the tiling function,
+// code/op_host/chunk_gated_delta_rule_fwd_h_tiling.cpp:152-261) and the kernel launch.
+#include "../../include/cgdr_fwd_h.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+
+#include "cgdr_kernels.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+cgdr_status fail(cgdr_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+constexpr int64_t kMaxHeadDim = 256;     // docs/problem.txt:466 (Triton wrapper assert K <= 256)
+constexpr int64_t kMaxValueDim = 1024;   // V-tiling lifts the reference's K == V <= 256
+constexpr int64_t kMaxTasks = 1 << 30;
+
+int env_int(const char* name, int dflt) {
+  const char* s = getenv(name);
+  if (s == nullptr || *s == 0) return dflt;
+  return atoi(s);
+}
+
+struct Plan {
+  int kernel;        // 0 bf16 pipeline, 1 fp32
+  int ncw;           // compute waves (Vt = 16 * ncw)
+  int stages;
+  int threads;
+  int lds;
+  int64_t tasks;
+};
+
+// Shape, stride and pointer checks shared by every entry point.
+cgdr_status validate(const cgdr_fwd_h_args* a) {
+  if (a == nullptr) return fail(CGDR_ERR_NULLPTR, "args is NULL");
+  if (a->k == nullptr) return fail(CGDR_ERR_NULLPTR, "Required input k is missing");
+  if (a->w == nullptr) return fail(CGDR_ERR_NULLPTR, "Required input w is missing");
+  if (a->u == nullptr) return fail(CGDR_ERR_NULLPTR, "Required input u is missing");
+  if (a->h == nullptr) return fail(CGDR_ERR_NULLPTR, "Required output h is missing");
+  if (a->chunk_size != CGDR_CHUNK_SIZE)
+    return fail(CGDR_ERR_UNSUPPORTED, "chunk_size must be %d, but got %lld", CGDR_CHUNK_SIZE,
+                (long long)a->chunk_size);
+  if (a->in_dtype != CGDR_BF16 && a->in_dtype != CGDR_F32)
+    return fail(CGDR_ERR_INVALID, "in_dtype %d is not a cgdr_dtype", a->in_dtype);
+  if (a->initial_state != nullptr && a->h0_dtype != CGDR_BF16 && a->h0_dtype != CGDR_F32)
+    return fail(CGDR_ERR_INVALID, "h0_dtype %d is not a cgdr_dtype", a->h0_dtype);
+  if (a->final_state != nullptr && a->final_dtype != CGDR_BF16 && a->final_dtype != CGDR_F32)
+    return fail(CGDR_ERR_INVALID, "final_dtype %d is not a cgdr_dtype", a->final_dtype);
+  if (a->B < 1) return fail(CGDR_ERR_INVALID, "B must be >= 1, but got %lld", (long long)a->B);
+  if (a->T < 1) return fail(CGDR_ERR_INVALID, "T must be >= 1, but got %lld", (long long)a->T);
+  if (a->H < 1 || a->Hg < 1)
+    return fail(CGDR_ERR_INVALID, "H/Hg are out of range: H=%lld, Hg=%lld", (long long)a->H, (long long)a->Hg);
+  if (a->H % a->Hg != 0)
+    return fail(CGDR_ERR_INVALID, "H must be divisible by Hg: H=%lld, Hg=%lld", (long long)a->H, (long long)a->Hg);
+  if (a->K < 1 || a->K > kMaxHeadDim)
+    return fail(CGDR_ERR_INVALID, "K must be in [1, %lld], but got %lld", (long long)kMaxHeadDim, (long long)a->K);
+  if (a->V < 1 || a->V > kMaxValueDim)
+    return fail(CGDR_ERR_INVALID, "V must be in [1, %lld], but got %lld", (long long)kMaxValueDim, (long long)a->V);
+
+  const int64_t nt_fixed = (a->T + CGDR_CHUNK_SIZE - 1) / CGDR_CHUNK_SIZE;
+  if (a->cu_seqlens == nullptr) {
+    if (a->chunk_offsets != nullptr)
+      return fail(CGDR_ERR_INVALID, "chunk_offsets given without cu_seqlens");
+    if (a->N != a->B)
+      return fail(CGDR_ERR_INVALID, "N must equal B without cu_seqlens: N=%lld, B=%lld", (long long)a->N, (long long)a->B);
+    if (a->NT != nt_fixed)
+      return fail(CGDR_ERR_INVALID, "NT must be ceil(T/64)=%lld, but got %lld", (long long)nt_fixed, (long long)a->NT);
+  } else {
+    if (a->B != 1) return fail(CGDR_ERR_INVALID, "B must be 1 with cu_seqlens, but got %lld", (long long)a->B);
+    if (a->N < 1) return fail(CGDR_ERR_INVALID, "N must be >= 1 with cu_seqlens, but got %lld", (long long)a->N);
+    if (a->N > a->T)
+      return fail(CGDR_ERR_INVALID, "The number of non-empty sequences cannot exceed T");
+    // code/op_host/chunk_gated_delta_rule_fwd_h_infershape.cpp:257-275
+    const int64_t lo = nt_fixed, hi = nt_fixed + a->N - 1;
+    if (a->NT < lo || a->NT > hi)
+      return fail(CGDR_ERR_INVALID, "NT=%lld is impossible for T=%lld and N=%lld; expected range [%lld, %lld]",
+                  (long long)a->NT, (long long)a->T, (long long)a->N, (long long)lo, (long long)hi);
+  }
+
+  // Strides: inner dims contiguous by contract; outer strides must be positive and large enough
+  // that rows do not overlap within one tensor.
+  const int64_t* sk = a->stride_k;
+  const int64_t* sw = a->stride_w;
+  const int64_t* su = a->stride_u;
+  const int64_t* sh = a->stride_h;
+  struct { const char* name; const int64_t* s; int64_t inner; bool present; } st3[] = {
+      {"k", sk, a->K, true}, {"w", sw, a->K, true}, {"u", su, a->V, true},
+      {"g", a->stride_g, 1, a->g != nullptr}, {"v_new", a->stride_v, a->V, a->v_new != nullptr},
+  };
+  for (auto& e : st3) {
+    if (!e.present) continue;
+    if (e.s[1] < 1 || e.s[2] < 1 || e.s[0] < 0)
+      return fail(CGDR_ERR_INVALID, "%s has non-positive strides (%lld, %lld, %lld)", e.name,
+                  (long long)e.s[0], (long long)e.s[1], (long long)e.s[2]);
+  }
+  if (sh[0] < 0 || sh[1] < a->K * a->V || sh[2] < a->K * a->V)
+    return fail(CGDR_ERR_INVALID, "h strides must keep K x V blocks apart");
+  if (a->initial_state != nullptr && (a->stride_h0[0] < 0 || a->stride_h0[1] < a->K * a->V))
+    return fail(CGDR_ERR_INVALID, "initial_state strides must keep K x V blocks apart");
+  if (a->final_state != nullptr && (a->stride_final[0] < 0 || a->stride_final[1] < a->K * a->V))
+    return fail(CGDR_ERR_INVALID, "final_state strides must keep K x V blocks apart");
+  return CGDR_OK;
+}
+
+int bf16_max_stages(int64_t K, int ncw);
+
+bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
+
+// Kernel variant and grid.  The bf16 pipeline needs K in {32,64,128,256} (MFMA contraction
+// slices of 32 and the LDS swizzles), V a multiple of 16, 16-byte aligned rows of k/w/u
+// (direct-to-LDS loads move 16 bytes per lane) and 8-byte aligned rows of h/v_new.
+cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
+  cgdr_status st = validate(a);
+  if (st != CGDR_OK) return st;
+  const int64_t K = a->K, V = a->V;
+  const int es = a->in_dtype == CGDR_BF16 ? 2 : 4;
+  if (!(K == 32 || K == 64 || K == 128 || K == 256))
+    return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (supported: 32, 64, 128, 256)", (long long)K);
+  if (V % 16 != 0)
+    return fail(CGDR_ERR_UNSUPPORTED, "V=%lld is not supported (must be a multiple of 16)", (long long)V);
+  if (a->in_dtype == CGDR_F32 && K > 128)
+    return fail(CGDR_ERR_UNSUPPORTED, "fp32 inputs support K <= 128, got K=%lld", (long long)K);
+  const int row_align = a->in_dtype == CGDR_BF16 ? 16 : 4;
+  const void* ptrs[] = {a->k, a->w, a->u};
+  const int64_t* strides[] = {a->stride_k, a->stride_w, a->stride_u};
+  for (int i = 0; i < 3; ++i) {
+    if (!aligned(ptrs[i], row_align))
+      return fail(CGDR_ERR_UNSUPPORTED, "k/w/u base pointers must be %d-byte aligned", row_align);
+    for (int d = 0; d < 3; ++d)
+      if ((strides[i][d] * es) % row_align != 0)
+        return fail(CGDR_ERR_UNSUPPORTED, "k/w/u strides must be multiples of %d bytes", row_align);
+  }
+  for (int i = 0; i < 3; ++i)
+    if (strides[i][1] * es * 64 >= ((int64_t)1 << 31))
+      return fail(CGDR_ERR_UNSUPPORTED, "k/w/u token strides must keep 64 rows within 2 GiB");
+  if (!aligned(a->h, 8) || (a->v_new != nullptr && !aligned(a->v_new, 8)))
+    return fail(CGDR_ERR_UNSUPPORTED, "h and v_new must be 8-byte aligned");
+  for (int d = 0; d < 3; ++d) {
+    if ((a->stride_h[d] * es) % 8 != 0 || (a->v_new != nullptr && (a->stride_v[d] * es) % 8 != 0))
+      return fail(CGDR_ERR_UNSUPPORTED, "h and v_new strides must be multiples of 8 bytes");
+  }
+
+  int ncw;
+  int forced = env_int("CGDR_FWD_H_VTILE", 0);
+  if (forced == 16 || forced == 32 || forced == 64) {
+    ncw = forced / 16;
+  } else {
+    // Enough workgroups to cover the 256 CUs first, then wider V-tiles (fewer K/W re-reads).
+    const int64_t pairs = a->N * a->H;
+    ncw = 1;
+    if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
+  }
+  if (V % (16 * ncw) != 0) ncw = 1;
+  if (a->in_dtype == CGDR_F32) {
+    pl->kernel = 1;
+    pl->ncw = ncw;
+    pl->stages = 1;
+    pl->threads = 64 * ncw;
+    pl->lds = 0;
+  } else {
+    pl->kernel = 0;
+    pl->ncw = ncw;
+    if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
+    pl->ncw = ncw;
+    int stages = env_int("CGDR_FWD_H_STAGES", 0);
+    // deepest ring that fits the LDS and the vmcnt range
+    const int max_stages = bf16_max_stages(K, ncw);
+    if (stages < 2 || stages > max_stages) stages = max_stages;
+    pl->stages = stages;
+    pl->threads = 64 * (ncw + 2);
+    pl->lds = 0;
+  }
+  pl->tasks = a->N * a->H * (V / (16 * ncw));
+  if (pl->tasks > kMaxTasks) return fail(CGDR_ERR_UNSUPPORTED, "too many tasks (%lld)", (long long)pl->tasks);
+  return CGDR_OK;
+}
+
+cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
+  cgdr::FwdHParams p;
+  memset(&p, 0, sizeof(p));
+  p.k = a->k; p.w = a->w; p.u = a->u; p.g = a->g; p.h0 = a->initial_state;
+  p.cu_seqlens = a->cu_seqlens; p.chunk_offsets = a->chunk_offsets;
+  p.h = a->h; p.v_new = a->v_new; p.final_state = a->final_state;
+  p.T = a->T; p.H = a->H; p.Hg = a->Hg; p.V = a->V; p.N = a->N; p.NT = a->NT;
+  p.sk_b = a->stride_k[0]; p.sk_t = a->stride_k[1]; p.sk_h = a->stride_k[2];
+  p.sw_b = a->stride_w[0]; p.sw_t = a->stride_w[1]; p.sw_h = a->stride_w[2];
+  p.su_b = a->stride_u[0]; p.su_t = a->stride_u[1]; p.su_h = a->stride_u[2];
+  p.sg_b = a->stride_g[0]; p.sg_t = a->stride_g[1]; p.sg_h = a->stride_g[2];
+  p.sh_b = a->stride_h[0]; p.sh_c = a->stride_h[1]; p.sh_h = a->stride_h[2];
+  p.sv_b = a->stride_v[0]; p.sv_t = a->stride_v[1]; p.sv_h = a->stride_v[2];
+  p.sh0_n = a->stride_h0[0]; p.sh0_h = a->stride_h0[1];
+  p.sf_n = a->stride_final[0]; p.sf_h = a->stride_final[1];
+  p.n_vtiles = (int)(a->V / (16 * pl.ncw));
+  p.n_tasks = (int)pl.tasks;
+  p.head_ratio = (int)(a->H / a->Hg);
+  p.h0_f32 = a->h0_dtype == CGDR_F32;
+  p.final_f32 = a->final_dtype == CGDR_F32;
+  p.has_g = a->g != nullptr;
+  return p;
+}
+
+template <int KD, int NCW, int STAGES>
+hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
+  using L = cgdr::Bf16Layout<KD, NCW, STAGES>;
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, STAGES>), dim3((unsigned)tasks), dim3(L::THREADS),
+                     0, stream, p);
+  return hipGetLastError();
+}
+
+template <int KD, int NCW>
+hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
+  using L = cgdr::F32Layout<KD, NCW>;
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int KD, int NCW>
+hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, 4>())
+    if (pl.stages == 4) return launch_bf16<KD, NCW, 4>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, 3>())
+    if (pl.stages == 3) return launch_bf16<KD, NCW, 3>(p, pl.tasks, s);
+  return launch_bf16<KD, NCW, 2>(p, pl.tasks, s);
+}
+
+int bf16_max_stages(int64_t K, int ncw) {
+  switch (K) {
+    case 32: return ncw == 1 ? cgdr::bf16_max_stages<32, 1>() : ncw == 2 ? cgdr::bf16_max_stages<32, 2>() : cgdr::bf16_max_stages<32, 4>();
+    case 64: return ncw == 1 ? cgdr::bf16_max_stages<64, 1>() : ncw == 2 ? cgdr::bf16_max_stages<64, 2>() : cgdr::bf16_max_stages<64, 4>();
+    case 128: return ncw == 1 ? cgdr::bf16_max_stages<128, 1>() : ncw == 2 ? cgdr::bf16_max_stages<128, 2>() : cgdr::bf16_max_stages<128, 4>();
+    default: return cgdr::bf16_max_stages<256, 1>();
+  }
+}
+
+template <int KD>
+hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  if constexpr (KD == 256) {
+    return dispatch_bf16_stages<KD, 1>(p, pl, s);
+  } else {
+    if (pl.ncw == 2) return dispatch_bf16_stages<KD, 2>(p, pl, s);
+    if (pl.ncw == 4) return dispatch_bf16_stages<KD, 4>(p, pl, s);
+    return dispatch_bf16_stages<KD, 1>(p, pl, s);
+  }
+}
+
+template <int KD>
+hipError_t dispatch_f32(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
+  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
+  return launch_f32<KD, 1>(p, pl.tasks, s);
+}
+
+int lds_bytes_of(const Plan& pl, int64_t K) {
+  if (pl.kernel == 1) {
+    switch (K) {
+      case 32: return pl.ncw == 1 ? cgdr::F32Layout<32, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<32, 2>::LDS_BYTES : cgdr::F32Layout<32, 4>::LDS_BYTES;
+      case 64: return pl.ncw == 1 ? cgdr::F32Layout<64, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<64, 2>::LDS_BYTES : cgdr::F32Layout<64, 4>::LDS_BYTES;
+      default: return pl.ncw == 1 ? cgdr::F32Layout<128, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<128, 2>::LDS_BYTES : cgdr::F32Layout<128, 4>::LDS_BYTES;
+    }
+  }
+  // bf16: the layout of the instantiated kernel
+  auto pick = [&](auto kd) -> int {
+    constexpr int KD = decltype(kd)::value;
+    auto by_stages = [&](auto ncw) -> int {
+      constexpr int NCW = decltype(ncw)::value;
+      if (pl.stages == 4) return cgdr::Bf16Layout<KD, NCW, 4>::LDS_BYTES;
+      if (pl.stages == 3) return cgdr::Bf16Layout<KD, NCW, 3>::LDS_BYTES;
+      return cgdr::Bf16Layout<KD, NCW, 2>::LDS_BYTES;
+    };
+    if (pl.ncw == 4) return by_stages(std::integral_constant<int, 4>{});
+    if (pl.ncw == 2) return by_stages(std::integral_constant<int, 2>{});
+    return by_stages(std::integral_constant<int, 1>{});
+  };
+  switch (K) {
+    case 32: return pick(std::integral_constant<int, 32>{});
+    case 64: return pick(std::integral_constant<int, 64>{});
+    case 128: return pick(std::integral_constant<int, 128>{});
+    default: return pick(std::integral_constant<int, 256>{});
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int cgdr_abi_version(void) { return CGDR_ABI_VERSION; }
+
+const char* cgdr_last_error(void) { return g_last_error; }
+
+const char* cgdr_status_string(cgdr_status status) {
+  switch (status) {
+    case CGDR_OK: return "CGDR_OK";
+    case CGDR_ERR_NULLPTR: return "CGDR_ERR_NULLPTR";
+    case CGDR_ERR_INVALID: return "CGDR_ERR_INVALID";
+    case CGDR_ERR_UNSUPPORTED: return "CGDR_ERR_UNSUPPORTED";
+    case CGDR_ERR_LAUNCH: return "CGDR_ERR_LAUNCH";
+  }
+  return "CGDR_ERR_UNKNOWN";
+}
+
+cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* workspace_bytes) {
+  if (workspace_bytes == nullptr) return fail(CGDR_ERR_NULLPTR, "workspace_bytes is NULL");
+  Plan pl;
+  cgdr_status st = make_plan(args, &pl);
+  if (st != CGDR_OK) return st;
+  *workspace_bytes = 0;
+  return CGDR_OK;
+}
+
+cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* plan) {
+  if (plan == nullptr) return fail(CGDR_ERR_NULLPTR, "plan is NULL");
+  Plan pl;
+  cgdr_status st = make_plan(args, &pl);
+  if (st != CGDR_OK) return st;
+  plan->kernel = pl.kernel;
+  plan->v_tile = 16 * pl.ncw;
+  plan->compute_waves = pl.ncw;
+  plan->total_waves = pl.threads / 64;
+  plan->stages = pl.stages;
+  plan->lds_bytes = lds_bytes_of(pl, args->K);
+  plan->workgroups = pl.tasks;
+  return CGDR_OK;
+}
+
+cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)workspace;
+  (void)workspace_bytes;
+  Plan pl;
+  cgdr_status st = make_plan(args, &pl);
+  if (st != CGDR_OK) return st;
+  const cgdr::FwdHParams p = to_params(args, pl);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipSuccess;
+  if (pl.kernel == 0) {
+    switch (args->K) {
+      case 32: e = dispatch_bf16<32>(p, pl, s); break;
+      case 64: e = dispatch_bf16<64>(p, pl, s); break;
+      case 128: e = dispatch_bf16<128>(p, pl, s); break;
+      default: e = dispatch_bf16<256>(p, pl, s); break;
+    }
+  } else {
+    switch (args->K) {
+      case 32: e = dispatch_f32<32>(p, pl, s); break;
+      case 64: e = dispatch_f32<64>(p, pl, s); break;
+      default: e = dispatch_f32<128>(p, pl, s); break;
+    }
+  }
+  if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
+  return CGDR_OK;
+}
+
+cgdr_status cgdr_prepare_chunk_offsets(const int64_t* cu_seqlens, int64_t n_seq, int64_t chunk_size,
+                                       int64_t* chunk_offsets_out) {
+  if (cu_seqlens == nullptr || chunk_offsets_out == nullptr)
+    return fail(CGDR_ERR_NULLPTR, "cu_seqlens and chunk_offsets_out are required");
+  if (n_seq < 0 || chunk_size < 1) return fail(CGDR_ERR_INVALID, "n_seq must be >= 0 and chunk_size >= 1");
+  if (n_seq >= 0 && cu_seqlens[0] != 0) return fail(CGDR_ERR_INVALID, "cu_seqlens must start at zero");
+  chunk_offsets_out[0] = 0;
+  for (int64_t i = 0; i < n_seq; ++i) {
+    const int64_t len = cu_seqlens[i + 1] - cu_seqlens[i];
+    if (len < 0) return fail(CGDR_ERR_INVALID, "cu_seqlens must be non-decreasing (entry %lld)", (long long)(i + 1));
+    chunk_offsets_out[i + 1] = chunk_offsets_out[i] + (len + chunk_size - 1) / chunk_size;
+  }
+  return CGDR_OK;
+}
+
+cgdr_status cgdr_prepare_chunk_indices(const int64_t* cu_seqlens, int64_t n_seq, int64_t chunk_size,
+                                       int64_t* chunk_indices_out, int64_t capacity_rows, int64_t* nt_out) {
+  if (cu_seqlens == nullptr || nt_out == nullptr) return fail(CGDR_ERR_NULLPTR, "cu_seqlens and nt_out are required");
+  if (n_seq < 0 || chunk_size < 1) return fail(CGDR_ERR_INVALID, "n_seq must be >= 0 and chunk_size >= 1");
+  if (cu_seqlens[0] != 0) return fail(CGDR_ERR_INVALID, "cu_seqlens must start at zero");
+  int64_t rows = 0;
+  for (int64_t i = 0; i < n_seq; ++i) {
+    const int64_t len = cu_seqlens[i + 1] - cu_seqlens[i];
+    if (len < 0) return fail(CGDR_ERR_INVALID, "cu_seqlens must be non-decreasing (entry %lld)", (long long)(i + 1));
+    const int64_t nc = (len + chunk_size - 1) / chunk_size;
+    for (int64_t c = 0; c < nc; ++c, ++rows) {
+      if (chunk_indices_out != nullptr) {
+        if (rows >= capacity_rows) return fail(CGDR_ERR_INVALID, "chunk_indices_out holds fewer than NT rows");
+        chunk_indices_out[2 * rows] = i;
+        chunk_indices_out[2 * rows + 1] = c;
+      }
+    }
+  }
+  *nt_out = rows;
+  return CGDR_OK;
+}
+
+}  // extern "C"

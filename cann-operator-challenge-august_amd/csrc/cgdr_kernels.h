@@ -1,0 +1,749 @@
+// cgdr_kernels.h -- gfx950 device code of the ChunkGatedDeltaRuleFwdH operator.
+//
+// One workgroup owns one task (sequence n, value head h, V-tile of 16*NCW columns) and
+// walks the chunks of its sequence in order.  The K x Vt fp32 state never leaves the
+// VGPRs of the compute waves.  Per chunk (docs/problem.txt:353-422 of the reference):
+//
+//   MM1  Vn = U - W bf16(S)             [64 x K] x [K x 16] per compute wave, bf16 MFMA
+//   v_new = bf16(Vn)                     (staged through LDS, stored by the store wave)
+//   Vd   = bf16(Vn * exp(g_last - g))    (safe_exp, docs/problem.txt:272-274)
+//   MM2  S = exp(g_last) S + K^T Vd      [K x 64] x [64 x 16] per compute wave
+//   h[c] = bf16(S entering the chunk)    (staged through LDS, stored by the store wave)
+//
+// Operand orientation is chosen so that neither the state nor Vd needs a layout change
+// between the two MFMAs: the MM2 accumulator (S) is directly the MM1 B operand after a
+// bf16 conversion, and the MM1 accumulator (Vn) is directly the MM2 B operand.  This
+// works because the row order inside an MFMA tile is free: MM2 tile kt row i holds
+// k = pi(kt, i) and MM1 tile tt row i holds token sigma(tt, i) with
+//     pi(2kb + hh, 4g + r)    = 32 kb + 8 g + 4 hh + r
+//     sigma(2tb + hh, 4g + r) = 32 tb + 8 g + 4 hh + r
+// so lane group g of two adjacent tiles holds 8 consecutive k (or tokens), which is the
+// 8-element contraction slice the v_mfma_f32_16x16x32_bf16 B operand wants.
+//
+// Roles inside a workgroup (wave index):
+//   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
+//   NCW         load wave: direct-to-LDS DMA of the W, K, U tiles of chunk c+STAGES-1,
+//               g of that chunk into VGPRs, gate factors of chunk c+1 into LDS
+//   NCW+1       store wave: h snapshot and v_new of chunk c-1 from LDS staging to HBM
+// One s_barrier per chunk hands stages over; no wave waits on another wave's memory
+// counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+namespace cgdr {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int kChunk = 64;
+
+// Kernel arguments (one kernarg block).  Strides are in elements.
+struct FwdHParams {
+  const void* k;
+  const void* w;
+  const void* u;
+  const float* g;
+  const void* h0;
+  const int64_t* cu_seqlens;
+  const int64_t* chunk_offsets;
+  void* h;
+  void* v_new;
+  void* final_state;
+  int64_t T, H, Hg, V, N, NT;
+  int64_t sk_b, sk_t, sk_h;
+  int64_t sw_b, sw_t, sw_h;
+  int64_t su_b, su_t, su_h;
+  int64_t sg_b, sg_t, sg_h;
+  int64_t sh_b, sh_c, sh_h;
+  int64_t sv_b, sv_t, sv_h;
+  int64_t sh0_n, sh0_h;
+  int64_t sf_n, sf_h;
+  int32_t n_vtiles;     // V / Vt
+  int32_t n_tasks;      // N * H * n_vtiles
+  int32_t head_ratio;   // H / Hg
+  int32_t h0_f32;       // initial_state dtype is fp32 (else bf16)
+  int32_t final_f32;    // final_state dtype is fp32 (else bf16)
+  int32_t has_g;
+};
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
+__device__ __forceinline__ constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | (7 << 4) | ((lgkm & 15) << 8) | (((vm >> 4) & 3) << 14);
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0)); }
+template <int VM>
+__device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(waitcnt_imm(VM, 15)); }
+
+// Workgroup barrier without the implied release/acquire fences of __syncthreads(): the
+// fences would make every wave drain its memory counters (vmcnt(0)), which would stall
+// the load wave's prefetches.  Each role waits for exactly what it hands over before
+// arriving.  The asm statements keep the compiler from moving memory operations across.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Direct-to-LDS DMA: each lane moves 16 (or 4) bytes from sbase + voff to LDS address
+// lds_addr + 16 * lane (4 * lane).  Written as asm so the compiler's waitcnt insertion does
+// not track it; callers wait with explicit s_waitcnt vmcnt.  M0 holds the LDS address.
+__device__ __forceinline__ void dma_b128(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
+}
+
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ float bf16_lo(unsigned x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned x) { return __uint_as_float(x & 0xffff0000u); }
+
+__device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? expf(x) : 0.f; }
+
+// ---------------------------------------------------------------------------------------------
+// Swizzles of 16-byte pieces inside LDS tiles (P = pieces per row).  Each is chosen so that the
+// 16 lanes of one MFMA lane group hit 16 distinct 16-byte bank groups of the 256-byte bank row.
+
+// W tile [64 tokens][K]: read by ds_read_b128, lanes i of a group read rows sigma(tt, i).
+template <int P>
+__device__ __forceinline__ int swz_w(int r) {
+  if constexpr (P == 4) return (r >> 3) & 3;
+  else if constexpr (P == 8) return ((r >> 1) & 1) | (((r >> 3) & 3) << 1);
+  else return (r & 3) | (((r >> 3) & 3) << 2);
+}
+// K tile [64 tokens][K]: read by ds_read_b64_tr_b16, lanes 4e+q read row R0+e, piece 4kb+q.
+template <int P>
+__device__ __forceinline__ int swz_k(int r) {
+  if constexpr (P == 4) return 0;
+  else if constexpr (P == 8) return 4 * ((r >> 1) & 1);
+  else return 4 * (r & 3);
+}
+// State staging [Vt rows = value columns][K]: written by ds_write_b128 from lanes n = 0..15.
+template <int P>
+__device__ __forceinline__ int swz_s(int v) {
+  if constexpr (P == 4) return (v >> 2) & 3;
+  else if constexpr (P == 8) return (v >> 1) & 7;
+  else return v & 15;
+}
+// v_new staging [Vt rows][64 tokens] (8 pieces per row).
+__device__ __forceinline__ int swz_v(int v) { return (v >> 1) & 7; }
+
+__device__ __forceinline__ f32x4 mfma_bf16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Task decoding shared by both kernels.  Workgroups are dealt to the 8 XCDs round-robin
+// (blockIdx % 8), so consecutive task ids are remapped onto one XCD: the V-tiles of a head,
+// and the heads sharing a key head, then share that XCD's L2 for their K and W reads.
+struct Task {
+  int n, head, vtile;
+  int64_t bos, len, boh;   // token offset, length, first chunk index of the sequence
+  int b;                   // batch row (fixed-length mode) or 0
+  int nc;                  // chunks this task walks (clamped so every write stays in bounds)
+};
+
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  const int q = nblocks >> 3, r = nblocks & 7;
+  const int xcd = bid & 7, local = bid >> 3;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
+}
+
+__device__ __forceinline__ Task decode_task(const FwdHParams& p, int task_id) {
+  Task t;
+  t.vtile = task_id % p.n_vtiles;
+  const int nh = task_id / p.n_vtiles;
+  t.head = nh % (int)p.H;
+  t.n = nh / (int)p.H;
+  if (p.cu_seqlens != nullptr) {
+    int64_t bos = p.cu_seqlens[t.n], eos = p.cu_seqlens[t.n + 1];
+    bos = bos < 0 ? 0 : (bos > p.T ? p.T : bos);
+    eos = eos < bos ? bos : (eos > p.T ? p.T : eos);
+    int64_t boh;
+    if (p.chunk_offsets != nullptr) {
+      boh = p.chunk_offsets[t.n];
+    } else {
+      boh = 0;
+      for (int m = 0; m < t.n; ++m) {
+        int64_t l = p.cu_seqlens[m + 1] - p.cu_seqlens[m];
+        boh += l > 0 ? (l + kChunk - 1) / kChunk : 0;
+      }
+    }
+    t.b = 0;
+    t.bos = bos;
+    t.len = eos - bos;
+    t.boh = boh;
+  } else {
+    t.b = t.n;
+    t.bos = 0;
+    t.len = p.T;
+    t.boh = 0;
+  }
+  int64_t nc = (t.len + kChunk - 1) / kChunk;
+  if (t.boh < 0 || t.boh >= p.NT) nc = 0;
+  else if (t.boh + nc > p.NT) nc = p.NT - t.boh;
+  t.nc = (int)nc;
+  return t;
+}
+
+// =============================================================================================
+// bf16 pipeline kernel.
+//   KD      key dim (32, 64, 128, 256)
+//   NCW     compute waves; Vt = 16 * NCW
+//   STAGES  LDS ring depth (chunks in flight: STAGES - 1 ahead of the compute waves)
+// =============================================================================================
+template <int KD, int NCW, int STAGES>
+struct Bf16Layout {
+  static constexpr int VT = 16 * NCW;
+  static constexpr int P = KD / 8;                 // 16-byte pieces per K row
+  static constexpr int W_OFF = 0;
+  static constexpr int K_OFF = 128 * KD;
+  static constexpr int U_OFF = 256 * KD;
+  static constexpr int G_OFF = 256 * KD + 128 * VT;            // gamma[64], a
+  static constexpr int GRAW_OFF = G_OFF + 512;                  // raw g row of the chunk
+  static constexpr int STAGE_BYTES = ((GRAW_OFF + 256) + 255) / 256 * 256;
+  static constexpr int SS_OFF = STAGES * STAGE_BYTES;          // state staging, 2 buffers
+  static constexpr int SS_BYTES = VT * KD * 2;
+  static constexpr int SV_OFF = SS_OFF + 2 * SS_BYTES;         // v_new staging, 2 buffers
+  static constexpr int SV_BYTES = VT * kChunk * 2;
+  static constexpr int LDS_BYTES = SV_OFF + 2 * SV_BYTES;
+  static constexpr int THREADS = 64 * (NCW + 2);
+  static constexpr int DMA_W = 128 * KD / 1024;               // DMA instructions per tile
+  static constexpr int DMA_U = (128 * VT + 1023) / 1024;
+};
+
+// A (KD, NCW, STAGES) configuration is valid when its LDS fits one gfx950 workgroup
+// (160 KiB) and the prefetch depth D = STAGES - 1 can be awaited with vmcnt (<= 63
+// outstanding VMEM instructions, PER_CHUNK per chunk).
+template <int KD, int NCW, int STAGES>
+constexpr bool bf16_config_ok() {
+  using L = Bf16Layout<KD, NCW, STAGES>;
+  constexpr int per_chunk = 2 * L::DMA_W + L::DMA_U + 1;
+  return STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES == 2 || (STAGES - 3) * per_chunk <= 63);
+}
+template <int KD, int NCW>
+constexpr int bf16_max_stages() {
+  return bf16_config_ok<KD, NCW, 4>() ? 4 : bf16_config_ok<KD, NCW, 3>() ? 3 : 2;
+}
+
+template <int KD, int NCW, int STAGES>
+__global__ void __launch_bounds__(64 * (NCW + 2))
+cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
+  using L = Bf16Layout<KD, NCW, STAGES>;
+  constexpr int VT = L::VT, P = L::P;
+  constexpr int KT = KD / 16;   // MM2 output tiles (rows of S)
+  constexpr int KB = KD / 32;   // MM1 contraction blocks
+  __shared__ __attribute__((aligned(1024))) char smem[L::LDS_BYTES];
+  static_assert(L::LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 workgroup exceeded");
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int task_id = xcd_remap(blockIdx.x, gridDim.x);
+  if (task_id >= p.n_tasks) return;   // uniform per workgroup
+  const Task tk = decode_task(p, task_id);
+  const int NC = tk.nc;
+  const int vbase = tk.vtile * VT;
+  const int hk = tk.head / p.head_ratio;
+
+  if (wave < NCW) {
+    // ------------------------------------------------------------------ compute wave
+    const int g = lane >> 4, n = lane & 15;
+    const int vcol = vbase + 16 * wave + n;      // value column owned by this lane
+    f32x4 S[KT];
+    if (p.h0 != nullptr) {
+      const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+          const int64_t off = base + (int64_t)krow * p.V + vcol;
+          S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off]
+                              : bf16_lo(((const unsigned short*)p.h0)[off]);
+        }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    block_barrier();   // P: stage 0 ready
+
+    for (int c = 0; c < NC; ++c) {
+      const int st = c % STAGES;
+      lds_char* stage = (lds_char*)smem + st * L::STAGE_BYTES;
+      const float* gam = (const float*)((char*)smem + st * L::STAGE_BYTES + L::G_OFF);
+      const float a = gam[64];
+
+      // bf16(S): MM1 B operands and the h snapshot.
+      bf16x8 Sb[KB];
+      u32x4 Sw[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        Sw[kb][0] = pack_bf16x2(S[2 * kb][0], S[2 * kb][1]);
+        Sw[kb][1] = pack_bf16x2(S[2 * kb][2], S[2 * kb][3]);
+        Sw[kb][2] = pack_bf16x2(S[2 * kb + 1][0], S[2 * kb + 1][1]);
+        Sw[kb][3] = pack_bf16x2(S[2 * kb + 1][2], S[2 * kb + 1][3]);
+        Sb[kb] = __builtin_bit_cast(bf16x8, Sw[kb]);
+      }
+      {
+        u32x4* ss = (u32x4*)(smem + L::SS_OFF + (c & 1) * L::SS_BYTES);
+        const int vrow = 16 * wave + n;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) ss[vrow * P + ((4 * kb + g) ^ swz_s<P>(vrow))] = Sw[kb];
+      }
+
+      // MM1: acc[tt] = W_tt bf16(S)
+      f32x4 acc[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
+        const u32x4* wrow = (const u32x4*)(smem + st * L::STAGE_BYTES + L::W_OFF) + row * P;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const u32x4 wv = wrow[(4 * kb + g) ^ swz_w<P>(row)];
+          acc[tt] = mfma_bf16(__builtin_bit_cast(bf16x8, wv), Sb[kb], acc[tt]);
+        }
+      }
+
+      // Epilogue: Vn = U - acc; v_new staging; Vd = bf16(Vn * gamma).
+      bf16x8 Vd[2];
+      {
+        u32x4* sv = (u32x4*)(smem + L::SV_OFF + (c & 1) * L::SV_BYTES);
+        const int vrow = 16 * wave + n;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          float vn[8];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            // U rows 32tb + 8g + 4hh + (0..3), column 16*wave + n, via a transposed read:
+            // source lane 4e+q addresses row t0+e, columns 16*wave + 4q .. +3.
+            const int e = n >> 2, q = n & 3;
+            const int t0 = 32 * tb + 8 * g + 4 * hh;
+            const lds_char* up = stage + L::U_OFF + ((t0 + e) * VT + 16 * wave + 4 * q) * 2;
+            const i16x4 uv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)up);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              vn[4 * hh + r] = __uint_as_float(((unsigned)(unsigned short)uv[r]) << 16) - acc[2 * tb + hh][r];
+          }
+          u32x4 pv, pd;
+          const f32x4 g0 = *(const f32x4*)(gam + 32 * tb + 8 * g);
+          const f32x4 g1 = *(const f32x4*)(gam + 32 * tb + 8 * g + 4);
+          const float gm[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            pv[j] = pack_bf16x2(vn[2 * j], vn[2 * j + 1]);
+            pd[j] = pack_bf16x2(vn[2 * j] * gm[2 * j], vn[2 * j + 1] * gm[2 * j + 1]);
+          }
+          sv[vrow * 8 + ((4 * tb + g) ^ swz_v(vrow))] = pv;
+          Vd[tb] = __builtin_bit_cast(bf16x8, pd);
+        }
+      }
+
+      // MM2: S = a S + K^T Vd
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        S[kt] = S[kt] * a;
+        const int kb = kt >> 1, hh = kt & 1;
+        const int e = n >> 2, q = n & 3;
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+          u32x4 ko;
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int row = 32 * tb + 8 * g + 4 * half + e;
+            const int piece = (4 * kb + q) ^ swz_k<P>(row);
+            const lds_char* kp = stage + L::K_OFF + (row * P + piece) * 16 + 8 * hh;
+            const i16x4 kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)kp);
+            const u32x2 kw = __builtin_bit_cast(u32x2, kv);
+            ko[2 * half] = kw[0];
+            ko[2 * half + 1] = kw[1];
+          }
+          S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, ko), Vd[tb], S[kt]);
+        }
+      }
+      wait_lgkm0();
+      block_barrier();   // B_c
+    }
+
+    if (p.final_state != nullptr) {
+      const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+          const int64_t off = base + (int64_t)krow * p.V + vcol;
+          if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
+          else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
+        }
+    }
+  } else if (wave == NCW) {
+    // ------------------------------------------------------------------ load wave
+    const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
+    const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
+    const __bf16* ubase = (const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
+    const float* gbase = p.g == nullptr ? nullptr : p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h;
+
+    // Per-lane byte offsets (within a chunk) of the 16-byte pieces each DMA instruction moves,
+    // hoisted out of the chunk loop: instruction m, lane -> LDS piece 64m + lane = (row r,
+    // slot s), filled from global piece (r, s ^ swizzle(r)).  With one scalar base per tile
+    // and chunk, every DMA is saddr + voffset (the host guarantees 64 rows span < 2 GiB).
+    constexpr int RPI = 64 / P;                 // rows per DMA instruction
+    constexpr int PU = VT / 8;                  // U pieces per row
+    const int lrow = lane / P, lcol = lane % P;
+    const int64_t stw = p.sw_t * 2, stk = p.sk_t * 2, stu = p.su_t * 2;   // row strides in bytes
+    uint32_t woff[L::DMA_W], koff[L::DMA_W], uoff[L::DMA_U];
+#pragma unroll
+    for (int m = 0; m < L::DMA_W; ++m) {
+      const int r = m * RPI + lrow;
+      woff[m] = (uint32_t)(r * stw) + 16u * (uint32_t)(lcol ^ swz_w<P>(r));
+      koff[m] = (uint32_t)(r * stk) + 16u * (uint32_t)(lcol ^ swz_k<P>(r));
+    }
+#pragma unroll
+    for (int m = 0; m < L::DMA_U; ++m) {
+      const int qd = 64 * m + lane;
+      uoff[m] = (uint32_t)((qd / PU) * stu) + 16u * (uint32_t)(qd % PU);
+    }
+    const char* wsrc = (const char*)wbase;
+    const char* ksrc = (const char*)kbase;
+    const char* usrc = (const char*)ubase;
+
+    // Issue the W, K, U tiles and the g row of chunk c into stage st.  Every load is a
+    // direct-to-LDS DMA written as inline asm: the compiler then tracks none of them, and
+    // the explicit in-order vmcnt waits below are the only waits (its own tracking cannot
+    // express more than 63 outstanding loads and would drain the whole pipeline instead).
+    // A partial (last) chunk takes a masked path: rows at or past the sequence end are
+    // zero-filled in LDS instead of loaded (the masked loads with other=0 of the reference).
+    const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
+    const bool has_g = gbase != nullptr;
+    const char* gsrc = has_g ? (const char*)gbase : (const char*)wbase;
+    const int64_t sgt = has_g ? p.sg_t * 4 : 0;
+    auto issue = [&](int c, int st) {
+      const int64_t t0 = tk.bos + (int64_t)c * kChunk;
+      const int64_t rem = tk.len - (int64_t)c * kChunk;
+      const int len = rem < kChunk ? (int)rem : kChunk;
+      const uint32_t lbase = lds0 + (uint32_t)(st * L::STAGE_BYTES);
+      char* sbase = smem + st * L::STAGE_BYTES;
+      const char* wchunk = wsrc + t0 * stw;
+      const char* kchunk = ksrc + t0 * stk;
+      const char* uchunk = usrc + t0 * stu;
+      const char* gchunk = gsrc + t0 * sgt;
+      const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
+      if (len == kChunk) {
+#pragma unroll
+        for (int m = 0; m < L::DMA_W; ++m) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
+#pragma unroll
+        for (int m = 0; m < L::DMA_W; ++m) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
+#pragma unroll
+        for (int m = 0; m < L::DMA_U; ++m) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
+      } else {
+#pragma unroll
+        for (int m = 0; m < L::DMA_W; ++m) {
+          if (m * RPI + lrow < len) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
+          else *(u32x4*)(sbase + L::W_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int m = 0; m < L::DMA_W; ++m) {
+          if (m * RPI + lrow < len) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
+          else *(u32x4*)(sbase + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int m = 0; m < L::DMA_U; ++m) {
+          if ((64 * m + lane) / PU < len) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
+          else *(u32x4*)(sbase + L::U_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      dma_b32(gchunk, goff, lbase + L::GRAW_OFF);
+    };
+    // Gate factors of chunk c into stage st from its raw g row: gamma_t = safe_exp(g_last - g_t)
+    // for t < len, 0 for padded rows, and a = exp(g_last) in slot 64.  No gating: gamma = 1, a = 1.
+    auto gates = [&](int c, int st) {
+      const int64_t rem = tk.len - (int64_t)c * kChunk;
+      const int len = rem < kChunk ? (int)rem : kChunk;
+      float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
+      float gamma, a;
+      if (has_g) {
+        const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
+        const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
+        gamma = lane < len ? safe_exp(glast - gv) : 0.f;
+        a = expf(glast);
+      } else {
+        gamma = lane < len ? 1.f : 0.f;
+        a = 1.f;
+      }
+      gdst[lane] = gamma;
+      if (lane == 0) gdst[64] = a;
+    };
+
+    // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
+    // completes loads in order, so the wait for chunk c+1 is "at most (D-2) full chunks
+    // outstanding" in steady state and vmcnt(0) near the end, where fewer chunks were issued.
+    constexpr int D = STAGES - 1;
+    constexpr int PER_CHUNK = 2 * L::DMA_W + L::DMA_U + 1;
+    static_assert(D >= 1, "at least one chunk of prefetch");
+    static_assert(D == 1 || (D - 2) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
+    constexpr int STEADY_VM = D >= 2 ? (D - 2) * PER_CHUNK : 0;
+
+    // Prologue: chunks 0 .. D-2 issued, chunk 0 landed and gated, then chunk D-1 issued,
+    // leaving chunks 1 .. D-1 in flight at the top of the loop.
+    if (NC > 0) {
+      if constexpr (D == 1) {
+        issue(0, 0);
+        wait_vm<0>();
+        gates(0, 0);
+      } else {
+        for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
+        if (D - 1 <= NC) wait_vm<STEADY_VM>();
+        else wait_vm<0>();
+        gates(0, 0);
+        if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
+      }
+    }
+    wait_lgkm0();
+    block_barrier();   // P
+
+    for (int c = 0; c < NC; ++c) {
+      if constexpr (D == 1) {
+        if (c + 1 < NC) {
+          issue(c + 1, (c + 1) % STAGES);
+          wait_vm<0>();
+          gates(c + 1, (c + 1) % STAGES);
+        }
+      } else {
+        if (c + 1 < NC) {
+          if (c + D <= NC) wait_vm<STEADY_VM>();
+          else wait_vm<0>();
+          gates(c + 1, (c + 1) % STAGES);
+        }
+        if (c + D < NC) issue(c + D, (c + D) % STAGES);
+      }
+      wait_lgkm0();
+      block_barrier();   // B_c
+    }
+  } else {
+    // ------------------------------------------------------------------ store wave
+    const int blk = lane >> 4, i = lane & 15;
+    const int e = i >> 2, q = i & 3;
+    __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
+    __bf16* vbase_ptr = p.v_new == nullptr ? nullptr
+                       : (__bf16*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h + vbase;
+
+    auto store_chunk = [&](int c) {
+      const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
+      // h snapshot: units of (16 k rows x 4 value columns) per 16-lane block.
+      const char* ss = smem + L::SS_OFF + (c & 1) * L::SS_BYTES;
+      __bf16* hdst = hbase + (tk.boh + c) * p.sh_c;
+      constexpr int UNITS_H = (KD / 16) * (VT / 4);
+#pragma unroll
+      for (int m = 0; m < UNITS_H / 4; ++m) {
+        const int unit = 4 * m + blk;
+        const int k0 = 16 * (unit / (VT / 4)), v0 = 4 * (unit % (VT / 4));
+        const int vrow = v0 + e;
+        const int kk = k0 + 4 * q;
+        const int piece = (kk >> 3) ^ swz_s<P>(vrow);
+        const lds_char* sp = (const lds_char*)ss + (vrow * P + piece) * 16 + 8 * ((kk >> 2) & 1);
+        const i16x4 hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp);
+        *(u32x2*)(hdst + (int64_t)(k0 + i) * p.V + v0) = __builtin_bit_cast(u32x2, hv);
+      }
+      if (vbase_ptr != nullptr) {
+        const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
+        __bf16* vdst = vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
+        constexpr int UNITS_V = 4 * (VT / 4);
+#pragma unroll
+        for (int m = 0; m < UNITS_V / 4; ++m) {
+          const int unit = 4 * m + blk;
+          const int t0 = 16 * (unit / (VT / 4)), v0 = 4 * (unit % (VT / 4));
+          const int vrow = v0 + e;
+          const int tt = t0 + 4 * q;
+          const int piece = (tt >> 3) ^ swz_v(vrow);
+          const lds_char* sp = (const lds_char*)sv + (vrow * 8 + piece) * 16 + 8 * ((tt >> 2) & 1);
+          const i16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp);
+          if (t0 + i < len) *(u32x2*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = __builtin_bit_cast(u32x2, vv);
+        }
+      }
+    };
+
+    block_barrier();   // P
+    for (int c = 0; c < NC; ++c) {
+      if (c >= 1) store_chunk(c - 1);
+      wait_lgkm0();
+      block_barrier();   // B_c
+    }
+    if (NC > 0) store_chunk(NC - 1);
+  }
+}
+
+// =============================================================================================
+// fp32 kernel (fp32 k/w/u/h/v_new): same task decomposition and the same tile orderings
+// (pi, sigma) with v_mfma_f32_16x16x4_f32, whose operands are one element per lane, so no
+// transposed reads are needed.  All waves load the next chunk with plain loads; it is the
+// exact-arithmetic path (fp32 products, fp32 accumulation) and is not the performance path.
+// =============================================================================================
+template <int KD, int NCW>
+struct F32Layout {
+  static constexpr int VT = 16 * NCW;
+  static constexpr int WP = KD + 4;     // padded row pitch (floats)
+  static constexpr int W_OFF = 0;
+  static constexpr int K_OFF = 64 * WP * 4;
+  static constexpr int U_OFF = 2 * 64 * WP * 4;
+  static constexpr int G_OFF = U_OFF + 64 * (VT + 4) * 4;
+  static constexpr int LDS_BYTES = G_OFF + 80 * 4;
+  static constexpr int THREADS = 64 * NCW;
+};
+
+template <int KD, int NCW>
+__global__ void __launch_bounds__(64 * NCW)
+cgdr_fwd_h_f32_kernel(const FwdHParams p) {
+  using L = F32Layout<KD, NCW>;
+  constexpr int VT = L::VT, WP = L::WP, UP = VT + 4;
+  constexpr int KT = KD / 16;
+  __shared__ __attribute__((aligned(16))) float smem[L::LDS_BYTES / 4];
+  float* Ws = smem + L::W_OFF / 4;
+  float* Ks = smem + L::K_OFF / 4;
+  float* Us = smem + L::U_OFF / 4;
+  float* Gs = smem + L::G_OFF / 4;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int task_id = xcd_remap(blockIdx.x, gridDim.x);
+  if (task_id >= p.n_tasks) return;
+  const Task tk = decode_task(p, task_id);
+  const int vbase = tk.vtile * VT;
+  const int hk = tk.head / p.head_ratio;
+  const int g = lane >> 4, n = lane & 15;
+  const int vcol = vbase + 16 * wave + n;
+
+  const float* kb_ = (const float*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
+  const float* wb_ = (const float*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
+  const float* ub_ = (const float*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
+  const float* gb_ = p.g == nullptr ? nullptr : p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h;
+  float* hb_ = (float*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h;
+  float* vb_ = p.v_new == nullptr ? nullptr : (float*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h;
+
+  f32x4 S[KT];
+  if (p.h0 != nullptr) {
+    const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+        const int64_t off = base + (int64_t)krow * p.V + vcol;
+        S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
+      }
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int c = 0; c < tk.nc; ++c) {
+    const int64_t t0 = tk.bos + (int64_t)c * kChunk;
+    const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
+      const int r = idx / KD, col = idx % KD;
+      Ws[r * WP + col] = r < len ? wb_[(t0 + r) * p.sw_t + col] : 0.f;
+      Ks[r * WP + col] = r < len ? kb_[(t0 + r) * p.sk_t + col] : 0.f;
+    }
+    for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
+      const int r = idx / VT, col = idx % VT;
+      Us[r * UP + col] = r < len ? ub_[(t0 + r) * p.su_t + col] : 0.f;
+    }
+    if (threadIdx.x < 64) {
+      const int t = threadIdx.x;
+      const float gv = (gb_ != nullptr && t < len) ? gb_[(t0 + t) * p.sg_t] : 0.f;
+      float gamma = t < len ? 1.f : 0.f, a = 1.f;
+      if (gb_ != nullptr) {
+        const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
+        gamma = t < len ? safe_exp(glast - gv) : 0.f;
+        a = expf(glast);
+      }
+      Gs[t] = gamma;
+      if (t == 0) Gs[64] = a;
+    }
+    __syncthreads();
+
+    // h snapshot (fp32, exact)
+    {
+      float* hdst = hb_ + (tk.boh + c) * p.sh_c;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+          hdst[(int64_t)krow * p.V + vcol] = S[kt][r];
+        }
+    }
+    // MM1: acc[tt] = W S   (contraction slot g of step (kt, r) is k = pi(kt, 4g + r))
+    f32x4 acc[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int kcol = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
+        const f32x4 wv = *(const f32x4*)(Ws + row * WP + kcol);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[tt] = mfma_f32(wv[r], S[kt][r], acc[tt]);
+      }
+    }
+    // Epilogue
+    const float a = Gs[64];
+    f32x4 Vd[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
+        const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
+        if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+        Vd[tt][r] = vn * Gs[t];
+      }
+    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r))
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      S[kt] = S[kt] * a;
+      const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
+          S[kt] = mfma_f32(Ks[t * WP + krow], Vd[tt][r], S[kt]);
+        }
+    }
+  }
+  if (p.final_state != nullptr) {
+    const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+        const int64_t off = base + (int64_t)krow * p.V + vcol;
+        if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
+        else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
+      }
+  }
+}
+
+}  // namespace cgdr

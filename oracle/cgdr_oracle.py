@@ -1,0 +1,358 @@
+"""CPU oracle for the ChunkGatedDeltaRuleFwdH chunk recurrence (numpy).
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product path (the HIP library behind ``include/cgdr_fwd_h.h``)
+never calls into it and never falls back to it.
+
+What it restates (paths relative to the reference's
+``ChunkGatedDeltaRuleFwdH_problem_290_template/``):
+
+* ``fwd_h(..., rounding=None)`` -- the exact recurrence ("O3"): the fp32 chunk
+  loop of ``ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_golden.py:136-149``
+  written against the FwdH inputs (w = k_cumdecay, u = value there).  Decay is
+  applied to ``v_new`` instead of ``k`` (``docs/problem.txt:400-405``), which is
+  the same product.  Output timing follows ``docs/problem.txt:81-167``:
+  ``h[c]`` is the state *entering* chunk c, ``v_new`` is the un-gated
+  ``U - W @ S`` and ``final`` the state after the last chunk.
+* ``fwd_h(..., rounding="bf16")`` -- the same loop with the rounding points of
+  the Triton kernel ``chunk_gated_delta_rule_fwd_kernel_h_blockdim64``
+  (``docs/problem.txt:330-432``, "O1"): ``bf16(S)`` feeds ``W @ S`` and the h
+  snapshot (``:356-360``, ``:392-394``), ``v_new`` is stored in the input dtype
+  (``:396-398``), the gated value is rounded to bf16 before ``K^T @ .``
+  (``:401-405``) and the state stays fp32.
+* ``prepare_chunk_offsets`` / ``prepare_chunk_indices`` -- ``docs/problem.txt:251-270``
+  and ``code/tests/golden/generate_golden.py:260-282``.
+* ``safe_exp`` -- ``docs/problem.txt:272-274``.
+* ``wy_prepare`` -- the producer of (w, u, g) from (k, v, beta, per-token
+  log-decay): ``chunk_gated_delta_rule_golden.py:102-124``.
+* ``gated_delta_rule_tokenwise`` -- the token-by-token Gated DeltaNet recurrence
+  ``S_t = e^{a_t} (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T``.  It is
+  not in the reference; it is the textbook definition that the chunked form
+  must reproduce, and the tests use it to pin ``fwd_h`` independently of any
+  chunked restatement.
+
+Layouts are token-major (FLA / Triton wrapper ``docs/problem.txt:434-472``):
+k ``[B,T,Hg,K]``, w ``[B,T,H,K]``, u ``[B,T,H,V]``, g ``[B,T,H]``,
+h0 ``[N,H,K,V]`` -> h ``[B,NT,H,K,V]``, v_new ``[B,T,H,V]``, final ``[N,H,K,V]``.
+``to_token_major`` / ``from_token_major`` convert the head-major layout of the
+contest reference ``run()`` (``docs/problem.txt:81-97``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+CHUNK_SIZE = 64
+
+
+# ----------------------------------------------------------------------------- rounding
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bfloat16 (ties to even), returned as float32.
+
+    NaN stays NaN; +-Inf and overflow follow IEEE round-to-nearest-even, which is
+    what ``torch.Tensor.to(torch.bfloat16)`` and ``v_cvt_pk_bf16_f32`` do.
+    """
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32)
+    # uint32 arithmetic wraps only for NaN payloads (>= 0xFFFF8000), which are restored below.
+    out = u >> 16
+    out &= 1
+    out += 0x7FFF
+    out += u
+    out &= np.uint32(0xFFFF0000)
+    out = out.view(np.float32)
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = np.nan
+    return out.reshape(x.shape)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """bfloat16 storage bits (uint16) of float32 values, ties to even."""
+    return (bf16_round(x).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(bits: np.ndarray) -> np.ndarray:
+    """float32 values of bfloat16 storage bits."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ----------------------------------------------------------------------------- varlen metadata
+
+def prepare_lens(cu_seqlens: np.ndarray) -> np.ndarray:
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    return cu[1:] - cu[:-1]
+
+
+def prepare_chunk_offsets(cu_seqlens: np.ndarray, chunk_size: int = CHUNK_SIZE) -> np.ndarray:
+    """``[0, C_0, C_0+C_1, ...]`` with ``C_n = ceil(L_n / chunk_size)``.
+
+    Follows ``docs/problem.txt:263-270`` (and ``:181-185``).
+    """
+    lens = prepare_lens(cu_seqlens)
+    counts = (lens + chunk_size - 1) // chunk_size
+    return np.concatenate([np.zeros(1, np.int64), np.cumsum(counts, dtype=np.int64)])
+
+
+def prepare_chunk_indices(cu_seqlens: np.ndarray, chunk_size: int = CHUNK_SIZE) -> np.ndarray:
+    """Rows ``(sequence, chunk-within-sequence)``, shape ``[NT, 2]`` int64.
+
+    Follows ``docs/problem.txt:251-261`` and ``code/tests/golden/generate_golden.py:260-270``.
+    """
+    rows = []
+    for n, length in enumerate(prepare_lens(cu_seqlens)):
+        rows.extend((n, c) for c in range(int((length + chunk_size - 1) // chunk_size)))
+    if not rows:
+        return np.zeros((0, 2), np.int64)
+    return np.asarray(rows, dtype=np.int64)
+
+
+def safe_exp(x: np.ndarray) -> np.ndarray:
+    """``exp(x)`` for ``x <= 0`` and ``0`` for ``x > 0`` (``docs/problem.txt:272-274``)."""
+    x = np.asarray(x)
+    return np.exp(np.where(x <= 0, x, -np.inf))
+
+
+# ----------------------------------------------------------------------------- layouts
+
+def to_token_major(w: np.ndarray, u: np.ndarray, g: np.ndarray | None):
+    """Head-major ``w [B,H,T,K]``, ``u [B,H,T,V]``, ``g [B,H,T]`` (``docs/problem.txt:216-219``)
+    to token-major.  ``k`` is ``[B,T,Hg,K]`` in both conventions."""
+    w_t = np.swapaxes(w, 1, 2)
+    u_t = np.swapaxes(u, 1, 2)
+    g_t = None if g is None else np.swapaxes(g, 1, 2)
+    return w_t, u_t, g_t
+
+
+def from_token_major(h: np.ndarray, v_new: np.ndarray | None):
+    """Token-major ``h [B,NT,H,K,V]`` / ``v_new [B,T,H,V]`` to the head-major outputs
+    ``[B,H,NT,K,V]`` / ``[B,H,T,V]`` of ``docs/problem.txt:94-96``."""
+    return np.swapaxes(h, 1, 2), None if v_new is None else np.swapaxes(v_new, 1, 2)
+
+
+# ----------------------------------------------------------------------------- the recurrence
+
+def sequence_bounds(B: int, T: int, cu_seqlens: np.ndarray | None, chunk_size: int = CHUNK_SIZE):
+    """Per sequence ``(batch_row, bos, eos, first_chunk)``; mirrors the bos/eos/boh
+    derivation of ``docs/problem.txt:336-350`` (varlen and fixed-length branches)."""
+    out = []
+    if cu_seqlens is None:
+        nt = (T + chunk_size - 1) // chunk_size
+        for b in range(B):
+            out.append((b, 0, T, 0, nt))  # each batch row owns chunks [b, 0:NT)
+        return out, nt
+    cu = np.asarray(cu_seqlens, dtype=np.int64)
+    offs = prepare_chunk_offsets(cu, chunk_size)
+    for n in range(cu.size - 1):
+        out.append((0, int(cu[n]), int(cu[n + 1]), int(offs[n]), None))
+    return out, int(offs[-1])
+
+
+def fwd_h(
+    k: np.ndarray,
+    w: np.ndarray,
+    u: np.ndarray,
+    g: np.ndarray | None = None,
+    initial_state: np.ndarray | None = None,
+    output_final_state: bool = True,
+    chunk_size: int = CHUNK_SIZE,
+    cu_seqlens: np.ndarray | None = None,
+    rounding: str | None = None,
+    compute_dtype=np.float32,
+    save_new_value: bool = True,
+):
+    """Chunked gated delta-rule state recurrence, token-major layouts.
+
+    ``rounding=None`` is the exact recurrence in ``compute_dtype``;
+    ``rounding="bf16"`` applies the bf16 rounding points of the Triton kernel
+    (the rounding model of the bf16 HIP kernel).  Inputs are taken as given
+    (bf16 inputs should be passed as their float32 values).
+
+    Returns ``(h, v_new, final)`` as arrays of ``compute_dtype``; ``h`` and
+    ``v_new`` are already rounded to bf16 values when ``rounding="bf16"``.
+    """
+    if chunk_size != CHUNK_SIZE:
+        raise ValueError(f"chunk_size must be {CHUNK_SIZE}, got {chunk_size}")
+    if rounding not in (None, "bf16"):
+        raise ValueError(f"unknown rounding {rounding!r}")
+    rnd = bf16_round if rounding == "bf16" else (lambda a: a)
+    cd = np.dtype(compute_dtype)
+
+    k = np.asarray(k, dtype=cd)
+    w = np.asarray(w, dtype=cd)
+    u = np.asarray(u, dtype=cd)
+    B, T, Hg, K = k.shape
+    H, V = u.shape[2], u.shape[3]
+    if w.shape != (B, T, H, K) or u.shape[:2] != (B, T):
+        raise ValueError("w must be [B,T,H,K] and u [B,T,H,V]")
+    if H % Hg != 0:
+        raise ValueError("H must be a multiple of Hg")
+    if cu_seqlens is not None and B != 1:
+        raise ValueError("cu_seqlens requires B == 1")
+    gq = None if g is None else np.asarray(g, dtype=cd)
+    head_of_key = np.arange(H) // (H // Hg)  # docs/problem_understanding.md:52-71
+
+    seqs, NT = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    N = len(seqs)
+    h_out = np.zeros((B, NT, H, K, V), dtype=cd)
+    v_out = np.zeros((B, T, H, V), dtype=cd) if save_new_value else None
+    final = np.zeros((N, H, K, V), dtype=cd) if output_final_state else None
+    h0 = None if initial_state is None else np.asarray(initial_state, dtype=cd)
+
+    for n, (b, bos, eos, boh, _) in enumerate(seqs):
+        S = np.zeros((H, K, V), dtype=cd) if h0 is None else h0[n].astype(cd, copy=True)
+        for c, t0 in enumerate(range(bos, eos, chunk_size)):
+            t1 = min(t0 + chunk_size, eos)
+            Sr = rnd(S) if rounding else S
+            h_out[b, boh + c] = Sr
+            Kc = np.transpose(k[b, t0:t1][:, head_of_key, :], (1, 0, 2))   # [H, L, K]
+            Wc = np.transpose(w[b, t0:t1], (1, 0, 2))                       # [H, L, K]
+            Uc = np.transpose(u[b, t0:t1], (1, 0, 2))                       # [H, L, V]
+            Vn = Uc - np.matmul(Wc, Sr)                                     # [H, L, V]
+            if save_new_value:
+                v_out[b, t0:t1] = np.transpose(rnd(Vn) if rounding else Vn, (1, 0, 2))
+            if gq is not None:
+                gc = np.transpose(gq[b, t0:t1], (1, 0))                     # [H, L]
+                g_last = gc[:, -1]
+                gamma = safe_exp(g_last[:, None] - gc).astype(cd)
+                Vd = Vn * gamma[:, :, None]
+                S = S * np.exp(g_last).astype(cd)[:, None, None]
+            else:
+                Vd = Vn
+            if rounding:
+                Vd = rnd(Vd)
+            S = S + np.matmul(np.transpose(Kc, (0, 2, 1)), Vd)
+        if output_final_state:
+            final[n] = S
+    return h_out, v_out, final
+
+
+# ----------------------------------------------------------------------------- producer / textbook recurrence
+
+def wy_prepare(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
+               chunk_size: int = CHUNK_SIZE, cu_seqlens: np.ndarray | None = None):
+    """(w, u, g) from keys, values, beta and per-token log-decay ``a`` (token-major).
+
+    Restates ``chunk_gated_delta_rule_golden.py:102-124`` in float64: per chunk
+    ``g = cumsum(a)`` (chunk-local), ``A = tril(beta_i k_i.k_j e^{g_i-g_j}, -1)``,
+    ``T = (I + A)^{-1}``, ``w = T (beta * e^g * k)``, ``u = T (beta * v)``.
+    The reference's forward-substitution loop (``:117-121``) is replaced by a
+    triangular solve, which is the same matrix.
+    k ``[B,T,H,K]`` (one key per value head), v ``[B,T,H,V]``, beta/a ``[B,T,H]``.
+    """
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    beta = np.asarray(beta, np.float64)
+    a = np.asarray(a, np.float64)
+    B, T, H, K = k.shape
+    w = np.zeros((B, T, H, K))
+    u = np.zeros(v.shape)
+    g = np.zeros((B, T, H))
+    seqs, _ = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    for (b, bos, eos, _, _) in seqs:
+        for t0 in range(bos, eos, chunk_size):
+            t1 = min(t0 + chunk_size, eos)
+            for hh in range(H):
+                kc, vc, bc = k[b, t0:t1, hh], v[b, t0:t1, hh], beta[b, t0:t1, hh]
+                gc = np.cumsum(a[b, t0:t1, hh])
+                L = t1 - t0
+                decay = np.exp(gc[:, None] - gc[None, :])
+                A = np.tril((bc[:, None] * (kc @ kc.T)) * decay, -1)
+                Tm = np.linalg.solve(np.eye(L) + A, np.eye(L))
+                w[b, t0:t1, hh] = Tm @ (bc[:, None] * np.exp(gc)[:, None] * kc)
+                u[b, t0:t1, hh] = Tm @ (bc[:, None] * vc)
+                g[b, t0:t1, hh] = gc
+    return w, u, g
+
+
+def gated_delta_rule_tokenwise(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
+                               initial_state: np.ndarray | None = None,
+                               chunk_size: int = CHUNK_SIZE,
+                               cu_seqlens: np.ndarray | None = None):
+    """Token-by-token Gated DeltaNet state recurrence in float64.
+
+    ``S_t = e^{a_t} (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T`` with
+    ``S`` of shape ``[K, V]``.  Returns the states entering every chunk,
+    ``[B, NT, H, K, V]``, and the final states ``[N, H, K, V]``.
+    """
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, T, H, K = k.shape
+    V = v.shape[-1]
+    seqs, NT = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    states = np.zeros((B, NT, H, K, V))
+    final = np.zeros((len(seqs), H, K, V))
+    for n, (b, bos, eos, boh, _) in enumerate(seqs):
+        for hh in range(H):
+            S = np.zeros((K, V)) if initial_state is None else np.array(initial_state[n, hh], np.float64)
+            for t in range(bos, eos):
+                if (t - bos) % chunk_size == 0:
+                    states[b, boh + (t - bos) // chunk_size, hh] = S
+                kt, vt = k[b, t, hh], v[b, t, hh]
+                S = np.exp(a[b, t, hh]) * S
+                S = S + beta[b, t, hh] * np.outer(kt, vt - S.T @ kt)
+            final[n, hh] = S
+    return states, final
+
+
+# ----------------------------------------------------------------------------- synthetic inputs
+
+def make_gate(rng: np.random.Generator, B: int, T: int, H: int, kind: str = "logsigmoid",
+              cu_seqlens: np.ndarray | None = None, chunk_size: int = CHUNK_SIZE, shift: float = 0.0):
+    """Chunk-local cumulative log-decay ``g [B,T,H]`` (non-increasing, <= 0 in every chunk).
+
+    kind="logsigmoid": cumsum of ``logsigmoid(randn + shift)`` restarted at every chunk
+    (BASELINE distributions; shift=-2 is the strongly decaying variant).
+    kind="linear": ``g = -rate * (1..L)`` with ``rate = 0.01 + 0.0025 (h % 5)``, the mild gate of
+    ``code/tests/golden/generate_golden.py:443-459``.
+    """
+    if kind == "logsigmoid":
+        z = rng.standard_normal((B, T, H)).astype(np.float32) + np.float32(shift)
+        inc = -np.logaddexp(np.float32(0.0), -z).astype(np.float32)
+    elif kind == "linear":
+        rate = (0.01 + 0.0025 * (np.arange(H) % 5)).astype(np.float32)
+        inc = np.broadcast_to(-rate, (B, T, H)).astype(np.float32)
+    else:
+        raise ValueError(kind)
+    g = np.zeros((B, T, H), np.float32)
+    seqs, _ = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    for (b, bos, eos, _, _) in seqs:
+        for t0 in range(bos, eos, chunk_size):
+            t1 = min(t0 + chunk_size, eos)
+            g[b, t0:t1] = np.cumsum(inc[b, t0:t1], axis=0, dtype=np.float32)
+    return g
+
+
+def make_inputs(seed: int, B: int, T: int, H: int, K: int, V: int, Hg: int | None = None,
+                dtype: str = "bf16", gate: str | None = "logsigmoid", gate_shift: float = 0.0,
+                with_h0: bool = True, cu_seqlens: np.ndarray | None = None, h0_scale: float = 0.1):
+    """Seeded synthetic FwdH inputs with the BASELINE distributions.
+
+    k = L2-normalised randn over K; w = randn * K^-1/2; u = randn; h0 = randn * h0_scale.
+    For dtype="bf16" k/w/u are rounded to bf16 values (float32 arrays holding bf16 values);
+    g and h0 are float32.
+    """
+    rng = np.random.default_rng(seed)
+    Hg = H if Hg is None else Hg
+    k = rng.standard_normal((B, T, Hg, K)).astype(np.float32)
+    k /= np.maximum(np.linalg.norm(k, axis=-1, keepdims=True), 1e-6)
+    w = (rng.standard_normal((B, T, H, K)) * K ** -0.5).astype(np.float32)
+    u = rng.standard_normal((B, T, H, V)).astype(np.float32)
+    N = B if cu_seqlens is None else len(cu_seqlens) - 1
+    h0 = (rng.standard_normal((N, H, K, V)) * h0_scale).astype(np.float32) if with_h0 else None
+    g = None if gate is None else make_gate(rng, B, T, H, gate, cu_seqlens, shift=gate_shift)
+    if dtype == "bf16":
+        k, w, u = bf16_round(k), bf16_round(w), bf16_round(u)
+    elif dtype != "f32":
+        raise ValueError(dtype)
+    return dict(k=k, w=w, u=u, g=g, initial_state=h0, cu_seqlens=cu_seqlens)
+
+
+def varlen_cu_seqlens(seed: int, n: int, lo: int, hi: int, chunk_size: int = CHUNK_SIZE) -> np.ndarray:
+    """``n`` seeded lengths uniform in ``[lo, hi]``, each moved off multiples of the chunk size."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(lo, hi + 1, size=n)
+    lens = np.where(lens % chunk_size == 0, lens + np.where(lens + 1 <= hi, 1, -1), lens)
+    return np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)

@@ -1,0 +1,168 @@
+"""C ABI checks that need no GPU: the library loads, exports what include/cgdr_fwd_h.h
+declares, the ctypes mirror matches the C struct layout, and host-side validation returns
+the documented status codes (mirroring the reference's infershape rejection cases,
+code/tests/ut/op_host/test_chunk_gated_delta_rule_fwd_h_infershape.cpp:137-223)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+from cgdr_amd import _abi
+from oracle import cgdr_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cgdr_fwd_h.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _abi.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    text = open(HEADER).read()
+    declared = set(re.findall(r"\b(cgdr_[a-z0-9_]+)\s*\(", text))
+    assert declared == set(_abi.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.cgdr_abi_version() == _abi.ABI_VERSION
+
+
+def test_struct_layout_matches_c(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(r'''
+#include <stdio.h>
+#include <stddef.h>
+#include "cgdr_fwd_h.h"
+#define F(s, f) printf(#s "." #f " %zu\n", offsetof(s, f))
+int main(void) {
+  printf("args %zu\nplan %zu\n", sizeof(cgdr_fwd_h_args), sizeof(cgdr_fwd_h_plan));
+  F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
+  F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, reserved0); F(cgdr_fwd_h_args, stride_k);
+  F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final);
+  F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups);
+  return 0;
+}''')
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)],
+                   check=True)
+    out = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                              check=True).stdout.split("\n") if line)
+    assert int(out["args"]) == ctypes.sizeof(_abi.FwdHArgs)
+    assert int(out["plan"]) == ctypes.sizeof(_abi.FwdHPlan)
+    for key, val in out.items():
+        if "." in key:
+            s, f = key.split(".")
+            cls = _abi.FwdHArgs if s == "cgdr_fwd_h_args" else _abi.FwdHPlan
+            assert getattr(cls, f).offset == int(val), key
+
+
+def _args(B=1, T=256, H=4, Hg=2, K=128, V=128, dtype=_abi.CGDR_BF16, varlen=None):
+    a = _abi.FwdHArgs()
+    fake = 1 << 24     # aligned, never dereferenced: validation is host-only
+    a.k = a.w = a.u = a.h = fake
+    a.B, a.T, a.H, a.Hg, a.K, a.V = B, T, H, Hg, K, V
+    a.chunk_size = 64
+    a.in_dtype = dtype
+    if varlen is None:
+        a.N, a.NT = B, (T + 63) // 64
+    else:
+        a.cu_seqlens = fake
+        a.N = len(varlen) - 1
+        a.NT = int(O.prepare_chunk_offsets(np.asarray(varlen))[-1])
+    a.stride_k[:] = [T * Hg * K, Hg * K, K]
+    a.stride_w[:] = [T * H * K, H * K, K]
+    a.stride_u[:] = [T * H * V, H * V, V]
+    a.stride_h[:] = [a.NT * H * K * V, H * K * V, K * V]
+    return a
+
+
+def _status(a):
+    n = ctypes.c_size_t(123)
+    return _abi.load().cgdr_fwd_h_workspace_size(ctypes.byref(a), ctypes.byref(n)), n.value
+
+
+def test_valid_args_need_no_workspace(lib):
+    assert _status(_args()) == (_abi.CGDR_OK, 0)
+    assert _status(_args(varlen=[0, 61, 64], T=64))[0] == _abi.CGDR_OK
+    assert _status(_args(dtype=_abi.CGDR_F32, K=64, V=64))[0] == _abi.CGDR_OK
+
+
+@pytest.mark.parametrize("mutate,expect", [
+    (lambda a: setattr(a, "k", None), _abi.CGDR_ERR_NULLPTR),
+    (lambda a: setattr(a, "w", None), _abi.CGDR_ERR_NULLPTR),
+    (lambda a: setattr(a, "u", None), _abi.CGDR_ERR_NULLPTR),
+    (lambda a: setattr(a, "h", None), _abi.CGDR_ERR_NULLPTR),
+    (lambda a: setattr(a, "chunk_size", 32), _abi.CGDR_ERR_UNSUPPORTED),
+    (lambda a: setattr(a, "Hg", 3), _abi.CGDR_ERR_INVALID),          # H % Hg != 0
+    (lambda a: setattr(a, "T", 0), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "NT", 5), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "N", 2), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "K", 300), _abi.CGDR_ERR_INVALID),         # K > 256
+    (lambda a: setattr(a, "K", 96), _abi.CGDR_ERR_UNSUPPORTED),
+    (lambda a: setattr(a, "V", 24), _abi.CGDR_ERR_UNSUPPORTED),
+    (lambda a: setattr(a, "in_dtype", 7), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "k", (1 << 24) + 8), _abi.CGDR_ERR_UNSUPPORTED),   # DMA needs 16B rows
+    (lambda a: setattr(a, "chunk_offsets", 1 << 24), _abi.CGDR_ERR_INVALID),  # without cu_seqlens
+])
+def test_rejections(lib, mutate, expect):
+    a = _args()
+    mutate(a)
+    st, _ = _status(a)
+    assert st == expect, (_abi.status_string(st), _abi.last_error())
+    assert _abi.last_error()
+
+
+def test_varlen_rejections(lib):
+    a = _args(varlen=[0, 61, 64], T=64)
+    a.B = 2
+    assert _status(a)[0] == _abi.CGDR_ERR_INVALID        # varlen needs B == 1
+    a = _args(varlen=[0, 61, 64], T=64)
+    a.NT = 3                                              # impossible for T=64, N=2
+    assert _status(a)[0] == _abi.CGDR_ERR_INVALID
+    assert "impossible" in _abi.last_error()
+
+
+def test_null_pointers_to_entry_points(lib):
+    n = ctypes.c_size_t(0)
+    assert lib.cgdr_fwd_h_workspace_size(None, ctypes.byref(n)) == _abi.CGDR_ERR_NULLPTR
+    assert lib.cgdr_fwd_h_workspace_size(ctypes.byref(_args()), None) == _abi.CGDR_ERR_NULLPTR
+    assert lib.cgdr_fwd_h_get_plan(ctypes.byref(_args()), None) == _abi.CGDR_ERR_NULLPTR
+
+
+def test_status_strings(lib):
+    assert _abi.status_string(_abi.CGDR_OK) == "CGDR_OK"
+    assert _abi.status_string(_abi.CGDR_ERR_LAUNCH) == "CGDR_ERR_LAUNCH"
+
+
+@pytest.mark.parametrize("cu", [[0, 61, 64], [0, 1], [0, 63, 127, 192, 1000], [0, 64, 128]])
+def test_host_chunk_metadata_matches_oracle(lib, cu):
+    assert _abi.prepare_chunk_offsets(cu) == O.prepare_chunk_offsets(np.asarray(cu)).tolist()
+    assert _abi.prepare_chunk_indices(cu) == [tuple(r) for r in O.prepare_chunk_indices(np.asarray(cu)).tolist()]
+
+
+def test_host_chunk_metadata_rejects_bad_cu(lib):
+    with pytest.raises(_abi.CgdrError):
+        _abi.prepare_chunk_offsets([1, 5])
+    with pytest.raises(_abi.CgdrError):
+        _abi.prepare_chunk_offsets([0, 5, 3])
+
+
+def test_plan_headline_fills_the_chip(lib):
+    p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128))
+    assert p.kernel == 0 and p.v_tile == 16 and p.workgroups == 256
+    assert p.lds_bytes <= 160 * 1024
+
+
+def test_wrapper_refuses_cpu_tensors():
+    import torch
+
+    import cgdr_amd
+    k = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
+    w = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, w)
