@@ -1,0 +1,178 @@
+"""Benchmark of the ChunkGatedDeltaRuleFwdH hot path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+A step is one FwdH call over the long-context prefill workload
+B=1, T=32768, H=Hg=32, K=V=128, bf16 k/w/u, fp32 g, h0=None, final state on
+(512 chunks per sequence walked inside the kernel).  Inputs are synthetic (seeded, the
+distributions of the CPU-runnable reference case) and resident in HBM before timing.
+Prints one JSON line: whole-job tokens/s, the dominant kernel's achieved HBM bandwidth
+against MI355X's 8 TB/s, and the CPU oracle (numpy restatement of the reference chunk loop)
+timed on this host's cores on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "cann-operator-challenge-august_amd"))
+
+METRIC = "tokens/sec + achieved HBM GB/s at B=1,T=32k,H=32,K=V=128 bf16 (1 GPU)"
+HBM_PEAK_GBPS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+WORKLOAD = dict(B=1, T=32768, H=32, Hg=32, K=128, V=128, chunk_size=64)
+
+
+def algorithmic_bytes(B, T, H, Hg, K, V, NT, N, s_in=2, s_out=2, h0_bytes=0, final_bytes=4):
+    """Each tensor counted once: k, w, u, g read; h, v_new, final written; h0 read if given."""
+    return (B * T * (Hg * K + H * K + H * V) * s_in + 4 * B * T * H + N * H * K * V * h0_bytes
+            + B * NT * H * K * V * s_out + B * T * H * V * s_out + N * H * K * V * final_bytes)
+
+
+def algorithmic_flops(B, NT, H, K, V):
+    return B * NT * H * 4 * 64 * K * V
+
+
+def make_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
+    """Synthetic inputs on the device: k L2-normalised randn, w = randn K^-1/2, u = randn,
+    g = chunk-local cumsum of logsigmoid(randn) (non-increasing, <= 0 within each chunk)."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    k = torch.randn(B, T, Hg, K, device=dev, generator=gen)
+    k = torch.nn.functional.normalize(k, dim=-1).to(torch.bfloat16)
+    w = (torch.randn(B, T, H, K, device=dev, generator=gen) * K ** -0.5).to(torch.bfloat16)
+    u = torch.randn(B, T, H, V, device=dev, generator=gen).to(torch.bfloat16)
+    inc = torch.nn.functional.logsigmoid(torch.randn(B, T, H, device=dev, generator=gen))
+    NT = (T + 63) // 64
+    pad = NT * 64 - T
+    inc = torch.nn.functional.pad(inc, (0, 0, 0, pad)).view(B, NT, 64, H)
+    g = inc.cumsum(dim=2).view(B, NT * 64, H)[:, :T].contiguous()
+    return k, w, u, g
+
+
+def cpu_baseline(torch, k, w, u, g, sample_heads: int, repeats: int = 3):
+    """Time the numpy oracle (exact fp32 chunk loop) on the host, on a head subset."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import cgdr_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    hs = slice(0, sample_heads)
+    kh = k[:, :, : max(1, sample_heads * k.shape[2] // w.shape[2])].float().cpu().numpy()
+    wh = w[:, :, hs].float().cpu().numpy()
+    uh = u[:, :, hs].float().cpu().numpy()
+    gh = g[:, :, hs].float().cpu().numpy()
+    times = []
+    with threadpool_limits(cores):
+        O.fwd_h(kh[:, :2048], wh[:, :2048], uh[:, :2048], gh[:, :2048])      # warm-up
+        for _ in range(repeats):
+            t0 = time.perf_counter()
+            O.fwd_h(kh, wh, uh, gh)
+            times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    tokens = k.shape[0] * k.shape[1]
+    frac = sample_heads / w.shape[2]
+    return dict(value=tokens * frac / t, unit="tokens/s", cores=cores, kind="port",
+                sample=f"numpy oracle (exact fp32 chunk loop), B=1 T={k.shape[1]} on {sample_heads} of "
+                       f"{w.shape[2]} heads, median of {repeats}; value scaled to all heads "
+                       f"({t:.2f} s per run)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-heads", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's path has no multi-GPU component "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import cgdr_amd
+
+    dev = torch.device("cuda:0")
+    W = WORKLOAD
+    B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
+    NT = (T + 63) // 64
+    k, w, u, g = make_inputs(torch, dev, B, T, H, Hg, K, V)
+    torch.cuda.synchronize()
+
+    def step():
+        return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, output_final_state=True)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_ms = sum(kern_ms) / len(kern_ms)
+
+    nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, B)
+    flops = algorithmic_flops(B, NT, H, K, V)
+    ms_per_step = wall * 1e3 / args.steps
+    tokens_per_s = B * T * args.steps / wall
+    achieved = nbytes / (avg_ms * 1e-3) / 1e9
+    plan = cgdr_amd.plan(k, u)
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "cgdr_fwd_h_bf16_T32768_H32_hbm_traffic.md")
+    if os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
+
+    out = {
+        "metric": METRIC,
+        "value": tokens_per_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "ChunkGatedDeltaRuleFwdH long-context prefill", **W,
+                   "h0": None, "output_final_state": True, "parallelism": "none (1 GPU)"},
+        "hbm_gbps": achieved,
+        "kernel_ms": avg_ms,
+        "kernel_ms_min": min(kern_ms),
+        "tflops": flops / (avg_ms * 1e-3) / 1e12,
+        "mfma_util": flops / (avg_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS,
+        "plan": plan,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
+                     "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads)
+        out["cpu_baseline"]["speedup"] = tokens_per_s / out["cpu_baseline"]["value"]
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -32,7 +32,7 @@ HIP_FLAGS = [
 ]
 
 SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip")]
-HEADERS = [os.path.join(CSRC, "cgdr_kernels.h"), os.path.join(REPO_ROOT, "include", "cgdr_fwd_h.h")]
+HEADERS = [os.path.join(CSRC, "cgdr_kernels.h"), os.path.join(CSRC, "cgdr_schedule.h"), os.path.join(REPO_ROOT, "include", "cgdr_fwd_h.h")]
 
 
 def build_library(verbose: bool = False) -> str:

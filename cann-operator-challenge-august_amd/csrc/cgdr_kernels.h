@@ -34,6 +34,8 @@
 
 #include <type_traits>
 
+#include "cgdr_schedule.h"
+
 namespace cgdr {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
@@ -496,7 +498,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 
     // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
     // completes loads in order, so the wait for chunk c+1 is "at most (D-2) full chunks
-    // outstanding" in steady state and vmcnt(0) near the end, where fewer chunks were issued.
+    // outstanding" while only full chunks follow it, and vmcnt(0) once the (possibly partial,
+    // hence shorter) last chunk of the sequence is among them (cgdr_schedule.h).
     constexpr int D = STAGES - 1;
     constexpr int PER_CHUNK = 2 * L::DMA_W + L::DMA_U + 1;
     static_assert(D >= 1, "at least one chunk of prefetch");
@@ -512,7 +515,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         gates(0, 0);
       } else {
         for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
-        if (D - 1 <= NC) wait_vm<STEADY_VM>();
+        if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
         else wait_vm<0>();
         gates(0, 0);
         if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
@@ -530,7 +533,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       } else {
         if (c + 1 < NC) {
-          if (c + D <= NC) wait_vm<STEADY_VM>();
+          if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
           else wait_vm<0>();
           gates(c + 1, (c + 1) % STAGES);
         }

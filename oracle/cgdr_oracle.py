@@ -327,22 +327,55 @@ def make_gate(rng: np.random.Generator, B: int, T: int, H: int, kind: str = "log
 
 def make_inputs(seed: int, B: int, T: int, H: int, K: int, V: int, Hg: int | None = None,
                 dtype: str = "bf16", gate: str | None = "logsigmoid", gate_shift: float = 0.0,
-                with_h0: bool = True, cu_seqlens: np.ndarray | None = None, h0_scale: float = 0.1):
-    """Seeded synthetic FwdH inputs with the BASELINE distributions.
+                with_h0: bool = True, cu_seqlens: np.ndarray | None = None, h0_scale: float = 0.1,
+                profile: str = "baseline"):
+    """Seeded synthetic FwdH inputs.
 
-    k = L2-normalised randn over K; w = randn * K^-1/2; u = randn; h0 = randn * h0_scale.
+    profile="baseline": k = L2-normalised randn over K; w = randn * K^-1/2; u = randn;
+        h0 = randn * h0_scale (the BASELINE distributions).  With a mild gate this w makes
+        the per-chunk state transition exp(g_last) I - K^T diag(gamma) W expansive
+        (spectral radius > 1), so long sequences amplify rounding differences; with the
+        BASELINE logsigmoid gate exp(g_last) ~ 1e-22 and every chunk starts afresh.
+    profile="golden": k, u ~ U(-1,1), w ~ U(-1,1)/K, h0 ~ randn * 0.25
+        (``code/tests/golden/generate_golden.py:472-490``); small w keeps the transition
+        contracting.
+    profile="wy": w, u produced by ``wy_prepare`` from L2-normalised keys, randn values,
+        beta = sigmoid(randn) and the gate's per-token log-decay: the inputs a Gated
+        DeltaNet layer really feeds this operator, whose transitions are contractions.
+        g is then the chunk-local cumsum of that decay (gate "logsigmoid" with gate_shift).
     For dtype="bf16" k/w/u are rounded to bf16 values (float32 arrays holding bf16 values);
     g and h0 are float32.
     """
     rng = np.random.default_rng(seed)
     Hg = H if Hg is None else Hg
-    k = rng.standard_normal((B, T, Hg, K)).astype(np.float32)
-    k /= np.maximum(np.linalg.norm(k, axis=-1, keepdims=True), 1e-6)
-    w = (rng.standard_normal((B, T, H, K)) * K ** -0.5).astype(np.float32)
-    u = rng.standard_normal((B, T, H, V)).astype(np.float32)
     N = B if cu_seqlens is None else len(cu_seqlens) - 1
-    h0 = (rng.standard_normal((N, H, K, V)) * h0_scale).astype(np.float32) if with_h0 else None
-    g = None if gate is None else make_gate(rng, B, T, H, gate, cu_seqlens, shift=gate_shift)
+    if profile == "baseline":
+        k = rng.standard_normal((B, T, Hg, K)).astype(np.float32)
+        k /= np.maximum(np.linalg.norm(k, axis=-1, keepdims=True), 1e-6)
+        w = (rng.standard_normal((B, T, H, K)) * K ** -0.5).astype(np.float32)
+        u = rng.standard_normal((B, T, H, V)).astype(np.float32)
+        h0 = (rng.standard_normal((N, H, K, V)) * h0_scale).astype(np.float32) if with_h0 else None
+        g = None if gate is None else make_gate(rng, B, T, H, gate, cu_seqlens, shift=gate_shift)
+    elif profile == "golden":
+        k = (rng.random((B, T, Hg, K)) * 2 - 1).astype(np.float32)
+        w = ((rng.random((B, T, H, K)) * 2 - 1) / K).astype(np.float32)
+        u = (rng.random((B, T, H, V)) * 2 - 1).astype(np.float32)
+        h0 = (rng.standard_normal((N, H, K, V)) * 0.25).astype(np.float32) if with_h0 else None
+        g = None if gate is None else make_gate(rng, B, T, H, gate, cu_seqlens, shift=gate_shift)
+    elif profile == "wy":
+        k = rng.standard_normal((B, T, Hg, K))
+        k /= np.maximum(np.linalg.norm(k, axis=-1, keepdims=True), 1e-6)
+        v = rng.standard_normal((B, T, H, V))
+        beta = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, T, H))))
+        z = rng.standard_normal((B, T, H)) + gate_shift
+        a = -np.logaddexp(0.0, -z) if gate is not None else np.zeros((B, T, H))
+        kfull = np.repeat(k, H // Hg, axis=2)
+        w, u, gc = wy_prepare(kfull, v, beta, a, cu_seqlens=cu_seqlens)
+        k, w, u = k.astype(np.float32), w.astype(np.float32), u.astype(np.float32)
+        g = None if gate is None else gc.astype(np.float32)
+        h0 = (rng.standard_normal((N, H, K, V)) * h0_scale).astype(np.float32) if with_h0 else None
+    else:
+        raise ValueError(profile)
     if dtype == "bf16":
         k, w, u = bf16_round(k), bf16_round(w), bf16_round(u)
     elif dtype != "f32":

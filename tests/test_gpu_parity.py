@@ -5,8 +5,11 @@ Tolerances (written per test):
   * bf16 inputs vs the bf16 rounding model of the reference Triton kernel
     (oracle rounding="bf16"): rtol=2e-2, atol=2e-3 elementwise.
   * bf16 inputs vs the exact fp32 recurrence: max error <= 1% of the tensor's scale (the
-    rounding model itself is that far from exact; elementwise 2e-2/2e-3 does not hold for
-    any bf16-operand implementation, see tests/test_oracle.py).
+    rounding model itself is that far from exact on random inputs; elementwise 2e-2/2e-3
+    does not hold there for any bf16-operand implementation, see tests/test_oracle.py),
+    and elementwise rtol=2e-2, atol=2e-3 for inputs made by the WY producer, whose
+    transitions contract as in a real Gated DeltaNet layer (at most a 1e-5 fraction of tail
+    elements outside; the rounding model alone reaches 0.9 of the bound there).
 Bit-exact identities: V-tile and pipeline-depth invariance, varlen = separate sequences,
 GQA = repeated keys, exact linearity, head-major = token-major.
 """
@@ -27,7 +30,9 @@ BF16_TOL = dict(rtol=2e-2, atol=2e-3)
 F32_TOL = dict(rtol=1e-4, atol=1e-5)
 
 
-def _check_bf16(d_out, inp, exact_frac=1e-2, names=("h", "v_new", "final")):
+def _check_bf16(d_out, inp, exact_frac=1e-2, names=("h", "v_new", "final"), exact_elementwise=False):
+    """vs the bf16 rounding model elementwise; vs the exact recurrence relative to scale, and
+    elementwise too for WY-produced inputs (contracting transitions)."""
     ref1 = O.fwd_h(**inp, rounding="bf16")
     ref3 = O.fwd_h(**inp)
     for name, got, r1, r3 in zip(names, d_out, ref1, ref3):
@@ -36,13 +41,22 @@ def _check_bf16(d_out, inp, exact_frac=1e-2, names=("h", "v_new", "final")):
         got = np32(got)
         assert_close(got, r1, name=f"{name} vs bf16 model", **BF16_TOL)
         assert_scale_close(got, r3, exact_frac, name=f"{name} vs exact")
+        if exact_elementwise:
+            # the rounding model itself sits at ~0.9 of this bound on WY inputs; allow a
+            # 1e-5 fraction of tail elements beyond it
+            bad = np.abs(got - r3) > BF16_TOL["atol"] + BF16_TOL["rtol"] * np.abs(r3)
+            assert bad.mean() <= 1e-5, f"{name} vs exact: {bad.sum()}/{bad.size} outside rtol=2e-2, atol=2e-3"
 
 
-def _case(seed, B, T, H, K, V, Hg=None, dtype="bf16", gate="logsigmoid", shift=0.0, h0=True, cu=None):
+def _case(seed, B, T, H, K, V, Hg=None, dtype="bf16", gate="logsigmoid", shift=0.0, h0=True, cu=None,
+          profile="baseline"):
+    """Inputs; profile "wy" (w, u from the WY producer) is used wherever a mild gate meets long
+    sequences, since BASELINE's random w makes those transitions expansive (see
+    oracle.cgdr_oracle.make_inputs)."""
     print(f"[case] seed={seed} B={B} T={T} H={H} Hg={Hg} K={K} V={V} dtype={dtype} gate={gate} "
-          f"shift={shift} h0={h0} varlen={cu is not None}", flush=True)
+          f"shift={shift} h0={h0} varlen={cu is not None} profile={profile}", flush=True)
     return O.make_inputs(seed, B, T, H, K, V, Hg=Hg, dtype=dtype, gate=gate, gate_shift=shift,
-                         with_h0=h0, cu_seqlens=cu)
+                         with_h0=h0, cu_seqlens=cu, profile=profile)
 
 
 # ---------------------------------------------------------------- BASELINE configurations
@@ -55,16 +69,20 @@ def test_config0_fp32(dev, gate):
         assert_close(np32(got), ref, name=name, **F32_TOL)
 
 
-@pytest.mark.parametrize("gate", ["logsigmoid", "linear"])
-def test_config1_bf16(dev, gate):
-    inp = _case(1, 2, 2048, 16, 128, 128, gate=gate)
+def test_config1_bf16(dev):
+    inp = _case(1, 2, 2048, 16, 128, 128)
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
+
+
+def test_config1_bf16_mild_decay_wy(dev):
+    inp = _case(11, 2, 2048, 16, 128, 128, shift=4.0, profile="wy")
+    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp, exact_elementwise=True)
 
 
 def test_config3_varlen_reduced(dev):
     cu = O.varlen_cu_seqlens(3, 16, 64, 1024)
-    inp = _case(3, 1, int(cu[-1]), 32, 128, 128, cu=cu, gate="linear")
-    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
+    inp = _case(3, 1, int(cu[-1]), 32, 128, 128, cu=cu, shift=4.0, profile="wy")
+    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp, exact_elementwise=True)
 
 
 def test_config4_wide_value_strong_decay(dev):
@@ -76,7 +94,7 @@ def test_config4_wide_value_strong_decay(dev):
 
 @pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (64, 128), (128, 64), (256, 256), (256, 64)])
 def test_head_dims_bf16(dev, K, V):
-    inp = _case(10 + K + V, 1, 200, 2, K, V, gate="linear")
+    inp = _case(10 + K + V, 1, 200, 2, K, V, shift=4.0, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
@@ -90,7 +108,7 @@ def test_head_dims_fp32(dev, K, V):
 
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 127, 128, 129])
 def test_chunk_boundaries(dev, T):
-    inp = _case(30 + T, 2, T, 2, 64, 64, gate="linear")
+    inp = _case(30 + T, 2, T, 2, 64, 64, shift=4.0, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
@@ -98,12 +116,12 @@ def test_chunk_boundaries(dev, T):
                                   [127, 128, 129, 1, 2, 3, 300]])
 def test_varlen_cases(dev, lens):
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    inp = _case(40 + len(lens), 1, int(cu[-1]), 4, 64, 64, Hg=2, gate="linear", cu=cu)
+    inp = _case(40 + len(lens), 1, int(cu[-1]), 4, 64, 64, Hg=2, shift=4.0, cu=cu, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
 def test_no_gate_no_initial_state(dev):
-    inp = _case(50, 1, 300, 4, 128, 128, gate=None, h0=False)
+    inp = _case(50, 1, 300, 4, 128, 128, gate=None, h0=False, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
@@ -253,3 +271,21 @@ def test_headline_shape_parity(dev):
     out2 = abi_call(d2)
     for x, y in zip(out, out2):
         assert torch.equal(x * 2, y)
+
+
+def test_partial_last_chunks_every_depth_deterministic(dev):
+    """Sequences of 1..5 chunks whose last chunk holds 1..64 rows, at every pipeline depth:
+    the load wave's waits must cover a partial last chunk in flight (it issues fewer DMA
+    instructions than a full one).  Repeated launches must be bit-identical."""
+    lens = [64 * j + r for j in range(5) for r in (1, 2, 17, 33, 63, 64)]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(80, 1, int(cu[-1]), 2, 64, 64, shift=4.0, cu=cu, profile="wy")
+    d = dev_inputs(inp, torch.bfloat16, dev)
+    ref1 = O.fwd_h(**inp, rounding="bf16")
+    for stages in (2, 3, 4):
+        outs = [_with_env("CGDR_FWD_H_STAGES", stages, lambda: abi_call(d)) for _ in range(3)]
+        for name, got, r in zip(("h", "v_new", "final"), outs[0], ref1):
+            assert_close(np32(got), r, name=f"{name} stages={stages}", **BF16_TOL)
+        for o in outs[1:]:
+            for a, b in zip(outs[0], o):
+                assert torch.equal(a, b), f"non-deterministic at stages={stages}"
