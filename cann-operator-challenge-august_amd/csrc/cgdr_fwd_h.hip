@@ -40,6 +40,7 @@ int env_int(const char* name, int dflt) {
 struct Plan {
   int kernel;        // 0 bf16 pipeline, 1 fp32
   int ncw;           // compute waves (Vt = 16 * ncw)
+  int nlw;           // load waves (bf16 pipeline)
   int stages;
   int threads;
   int lds;
@@ -118,7 +119,7 @@ cgdr_status validate(const cgdr_fwd_h_args* a) {
   return CGDR_OK;
 }
 
-int bf16_max_stages(int64_t K, int ncw);
+int bf16_max_stages(int64_t K, int ncw, int nlw);
 
 bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
 
@@ -170,6 +171,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   if (a->in_dtype == CGDR_F32) {
     pl->kernel = 1;
     pl->ncw = ncw;
+    pl->nlw = 0;
     pl->stages = 1;
     pl->threads = 64 * ncw;
     pl->lds = 0;
@@ -178,12 +180,15 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     pl->ncw = ncw;
     if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
+    int nlw = env_int("CGDR_FWD_H_LOADERS", 0);
+    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = 2;
+    pl->nlw = nlw;
     int stages = env_int("CGDR_FWD_H_STAGES", 0);
     // deepest ring that fits the LDS and the vmcnt range
-    const int max_stages = bf16_max_stages(K, ncw);
+    const int max_stages = bf16_max_stages(K, ncw, nlw);
     if (stages < 2 || stages > max_stages) stages = max_stages;
     pl->stages = stages;
-    pl->threads = 64 * (ncw + 2);
+    pl->threads = 64 * (ncw + nlw + 2);
     pl->lds = 0;
   }
   pl->tasks = a->N * a->H * (V / (16 * ncw));
@@ -212,14 +217,15 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.h0_f32 = a->h0_dtype == CGDR_F32;
   p.final_f32 = a->final_dtype == CGDR_F32;
   p.has_g = a->g != nullptr;
+  p.prefetch = env_int("CGDR_FWD_H_PREFETCH", 4);
   return p;
 }
 
-template <int KD, int NCW, int STAGES>
+template <int KD, int NCW, int NLW, int STAGES>
 hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
-  using L = cgdr::Bf16Layout<KD, NCW, STAGES>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, STAGES>), dim3((unsigned)tasks), dim3(L::THREADS),
-                     0, stream, p);
+  using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES>), dim3((unsigned)tasks),
+                     dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -230,32 +236,71 @@ hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stre
   return hipGetLastError();
 }
 
-template <int KD, int NCW>
+template <int KD, int NCW, int NLW>
 hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, 4>())
-    if (pl.stages == 4) return launch_bf16<KD, NCW, 4>(p, pl.tasks, s);
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, 3>())
-    if (pl.stages == 3) return launch_bf16<KD, NCW, 3>(p, pl.tasks, s);
-  return launch_bf16<KD, NCW, 2>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4>())
+    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3>())
+    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3>(p, pl.tasks, s);
+  return launch_bf16<KD, NCW, NLW, 2>(p, pl.tasks, s);
 }
 
-int bf16_max_stages(int64_t K, int ncw) {
-  switch (K) {
-    case 32: return ncw == 1 ? cgdr::bf16_max_stages<32, 1>() : ncw == 2 ? cgdr::bf16_max_stages<32, 2>() : cgdr::bf16_max_stages<32, 4>();
-    case 64: return ncw == 1 ? cgdr::bf16_max_stages<64, 1>() : ncw == 2 ? cgdr::bf16_max_stages<64, 2>() : cgdr::bf16_max_stages<64, 4>();
-    case 128: return ncw == 1 ? cgdr::bf16_max_stages<128, 1>() : ncw == 2 ? cgdr::bf16_max_stages<128, 2>() : cgdr::bf16_max_stages<128, 4>();
-    default: return cgdr::bf16_max_stages<256, 1>();
-  }
+template <int KD, int NCW>
+hipError_t dispatch_bf16_nlw(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1>(p, pl, s);
+  if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4>(p, pl, s);
+  return dispatch_bf16_stages<KD, NCW, 2>(p, pl, s);
 }
 
 template <int KD>
 hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (KD == 256) {
-    return dispatch_bf16_stages<KD, 1>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1>(p, pl, s);
   } else {
-    if (pl.ncw == 2) return dispatch_bf16_stages<KD, 2>(p, pl, s);
-    if (pl.ncw == 4) return dispatch_bf16_stages<KD, 4>(p, pl, s);
-    return dispatch_bf16_stages<KD, 1>(p, pl, s);
+    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2>(p, pl, s);
+    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1>(p, pl, s);
+  }
+}
+
+// Compile-time layout facts of the bf16 kernel instantiation a plan selects.
+template <int KD, typename F>
+auto with_bf16_config(const Plan& pl, F f) {
+  auto by_nlw = [&](auto ncw) {
+    constexpr int NCW = decltype(ncw)::value;
+    auto by_stages = [&](auto nlw) {
+      constexpr int NLW = decltype(nlw)::value;
+      if (pl.stages == 4) return f(cgdr::Bf16Layout<KD, NCW, NLW, 4>{});
+      if (pl.stages == 3) return f(cgdr::Bf16Layout<KD, NCW, NLW, 3>{});
+      return f(cgdr::Bf16Layout<KD, NCW, NLW, 2>{});
+    };
+    if (pl.nlw == 1) return by_stages(std::integral_constant<int, 1>{});
+    if (pl.nlw == 4) return by_stages(std::integral_constant<int, 4>{});
+    return by_stages(std::integral_constant<int, 2>{});
+  };
+  if (pl.ncw == 4) return by_nlw(std::integral_constant<int, 4>{});
+  if (pl.ncw == 2) return by_nlw(std::integral_constant<int, 2>{});
+  return by_nlw(std::integral_constant<int, 1>{});
+}
+
+int bf16_max_stages(int64_t K, int ncw, int nlw) {
+  auto pick = [&](auto kd) -> int {
+    constexpr int KD = decltype(kd)::value;
+    auto by_ncw = [&](auto c) -> int {
+      constexpr int NCW = decltype(c)::value;
+      if (nlw == 1) return cgdr::bf16_max_stages<KD, NCW, 1>();
+      if (nlw == 4) return cgdr::bf16_max_stages<KD, NCW, 4>();
+      return cgdr::bf16_max_stages<KD, NCW, 2>();
+    };
+    if (ncw == 4) return by_ncw(std::integral_constant<int, 4>{});
+    if (ncw == 2) return by_ncw(std::integral_constant<int, 2>{});
+    return by_ncw(std::integral_constant<int, 1>{});
+  };
+  switch (K) {
+    case 32: return pick(std::integral_constant<int, 32>{});
+    case 64: return pick(std::integral_constant<int, 64>{});
+    case 128: return pick(std::integral_constant<int, 128>{});
+    default: return pick(std::integral_constant<int, 256>{});
   }
 }
 
@@ -275,23 +320,12 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
     }
   }
   // bf16: the layout of the instantiated kernel
-  auto pick = [&](auto kd) -> int {
-    constexpr int KD = decltype(kd)::value;
-    auto by_stages = [&](auto ncw) -> int {
-      constexpr int NCW = decltype(ncw)::value;
-      if (pl.stages == 4) return cgdr::Bf16Layout<KD, NCW, 4>::LDS_BYTES;
-      if (pl.stages == 3) return cgdr::Bf16Layout<KD, NCW, 3>::LDS_BYTES;
-      return cgdr::Bf16Layout<KD, NCW, 2>::LDS_BYTES;
-    };
-    if (pl.ncw == 4) return by_stages(std::integral_constant<int, 4>{});
-    if (pl.ncw == 2) return by_stages(std::integral_constant<int, 2>{});
-    return by_stages(std::integral_constant<int, 1>{});
-  };
+  auto lds = [](auto layout) -> int { return decltype(layout)::LDS_BYTES; };
   switch (K) {
-    case 32: return pick(std::integral_constant<int, 32>{});
-    case 64: return pick(std::integral_constant<int, 64>{});
-    case 128: return pick(std::integral_constant<int, 128>{});
-    default: return pick(std::integral_constant<int, 256>{});
+    case 32: return with_bf16_config<32>(pl, lds);
+    case 64: return with_bf16_config<64>(pl, lds);
+    case 128: return with_bf16_config<128>(pl, lds);
+    default: return with_bf16_config<256>(pl, lds);
   }
 }
 

@@ -22,9 +22,10 @@
 //
 // Roles inside a workgroup (wave index):
 //   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
-//   NCW         load wave: direct-to-LDS DMA of the W, K, U tiles of chunk c+STAGES-1,
-//               g of that chunk into VGPRs, gate factors of chunk c+1 into LDS
-//   NCW+1       store wave: h snapshot and v_new of chunk c-1 from LDS staging to HBM
+//   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles and the g row of
+//               chunk c+STAGES-1 (shared round-robin), gate factors of chunk c+1 into LDS
+//   NCW+NLW     store wave: h snapshot and v_new of chunk c-1 from LDS staging to HBM
+//   NCW+NLW+1   prefetch wave: touches chunk c+prefetch into L2
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
 #pragma once
@@ -75,6 +76,8 @@ struct FwdHParams {
   int32_t h0_f32;       // initial_state dtype is fp32 (else bf16)
   int32_t final_f32;    // final_state dtype is fp32 (else bf16)
   int32_t has_g;
+  int32_t prefetch;     // L2 prefetch distance in chunks (0: off)
+  int32_t reserved;
 };
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
@@ -101,6 +104,11 @@ __device__ __forceinline__ void block_barrier() {
 __device__ __forceinline__ void dma_b128(const void* sbase, uint32_t voff, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(sbase), "s"(lds_addr) : "memory", "m0");
+}
+// 4 bytes per lane from a per-lane 64-bit address (used to touch lines into L2).
+__device__ __forceinline__ void dma_b32_addr(const void* addr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(addr), "s"(lds_addr) : "memory", "m0");
 }
 __device__ __forceinline__ void dma_b32(const void* sbase, uint32_t voff, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
@@ -211,9 +219,10 @@ __device__ __forceinline__ Task decode_task(const FwdHParams& p, int task_id) {
 // bf16 pipeline kernel.
 //   KD      key dim (32, 64, 128, 256)
 //   NCW     compute waves; Vt = 16 * NCW
+//   NLW     load waves (1, 2 or 4)
 //   STAGES  LDS ring depth (chunks in flight: STAGES - 1 ahead of the compute waves)
 // =============================================================================================
-template <int KD, int NCW, int STAGES>
+template <int KD, int NCW, int NLW, int STAGES>
 struct Bf16Layout {
   static constexpr int VT = 16 * NCW;
   static constexpr int P = KD / 8;                 // 16-byte pieces per K row
@@ -227,30 +236,38 @@ struct Bf16Layout {
   static constexpr int SS_BYTES = VT * KD * 2;
   static constexpr int SV_OFF = SS_OFF + 2 * SS_BYTES;         // v_new staging, 2 buffers
   static constexpr int SV_BYTES = VT * kChunk * 2;
-  static constexpr int LDS_BYTES = SV_OFF + 2 * SV_BYTES;
-  static constexpr int THREADS = 64 * (NCW + 2);
+  static constexpr int TRASH_OFF = SV_OFF + 2 * SV_BYTES;      // L2-prefetch landing area
+  static constexpr int LDS_BYTES = TRASH_OFF + 256;
+  static constexpr int THREADS = 64 * (NCW + NLW + 2);
   static constexpr int DMA_W = 128 * KD / 1024;               // DMA instructions per tile
   static constexpr int DMA_U = (128 * VT + 1023) / 1024;
+  static constexpr int DMA_TILES = 2 * DMA_W + DMA_U;         // per chunk, over all load waves
+  // DMA instructions load wave lw issues per full chunk: tile instruction i goes to wave
+  // i % NLW, and wave 0 also moves the g row.
+  template <int LW>
+  static constexpr int dma_per_chunk() {
+    return DMA_TILES / NLW + (LW < DMA_TILES % NLW ? 1 : 0) + (LW == 0 ? 1 : 0);
+  }
 };
 
-// A (KD, NCW, STAGES) configuration is valid when its LDS fits one gfx950 workgroup
-// (160 KiB) and the prefetch depth D = STAGES - 1 can be awaited with vmcnt (<= 63
-// outstanding VMEM instructions, PER_CHUNK per chunk).
-template <int KD, int NCW, int STAGES>
+// A configuration is valid when its LDS fits one gfx950 workgroup (160 KiB) and the prefetch
+// depth D = STAGES - 1 can be awaited with vmcnt (<= 63 outstanding VMEM instructions per
+// wave; load wave 0 carries the most per chunk).
+template <int KD, int NCW, int NLW, int STAGES>
 constexpr bool bf16_config_ok() {
-  using L = Bf16Layout<KD, NCW, STAGES>;
-  constexpr int per_chunk = 2 * L::DMA_W + L::DMA_U + 1;
+  using L = Bf16Layout<KD, NCW, NLW, STAGES>;
+  constexpr int per_chunk = L::template dma_per_chunk<0>();
   return STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES == 2 || (STAGES - 3) * per_chunk <= 63);
 }
-template <int KD, int NCW>
+template <int KD, int NCW, int NLW>
 constexpr int bf16_max_stages() {
-  return bf16_config_ok<KD, NCW, 4>() ? 4 : bf16_config_ok<KD, NCW, 3>() ? 3 : 2;
+  return bf16_config_ok<KD, NCW, NLW, 4>() ? 4 : bf16_config_ok<KD, NCW, NLW, 3>() ? 3 : 2;
 }
 
-template <int KD, int NCW, int STAGES>
-__global__ void __launch_bounds__(64 * (NCW + 2))
+template <int KD, int NCW, int NLW, int STAGES>
+__global__ void __launch_bounds__(64 * (NCW + NLW + 2))
 cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
-  using L = Bf16Layout<KD, NCW, STAGES>;
+  using L = Bf16Layout<KD, NCW, NLW, STAGES>;
   constexpr int VT = L::VT, P = L::P;
   constexpr int KT = KD / 16;   // MM2 output tiles (rows of S)
   constexpr int KB = KD / 32;   // MM1 contraction blocks
@@ -290,20 +307,47 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 
     for (int c = 0; c < NC; ++c) {
       const int st = c % STAGES;
-      lds_char* stage = (lds_char*)smem + st * L::STAGE_BYTES;
-      const float* gam = (const float*)((char*)smem + st * L::STAGE_BYTES + L::G_OFF);
-      const float a = gam[64];
+      const char* sbase = smem + st * L::STAGE_BYTES;
+      const lds_char* stage = (const lds_char*)sbase;
+      const float* gam = (const float*)(sbase + L::G_OFF);
+      const int e = n >> 2, q = n & 3;
 
-      // bf16(S): MM1 B operands and the h snapshot.
-      bf16x8 Sb[KB];
+      // Phase 1: every LDS read MM1 and the epilogue need (a, gamma, U, W operands) is issued
+      // up front, so their latency hides under the bf16 conversion and the first MFMAs.
+      const float a = gam[64];
+      f32x4 gm[2][2];                 // gamma of tokens 32 tb + 8 g + 4 hh + (0..3)
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) gm[tb][hh] = *(const f32x4*)(gam + 32 * tb + 8 * g + 4 * hh);
+      // U rows sigma(tt, 4g + r), column 16*wave + n, by a transposed read: source lane 4e+q
+      // addresses row t0+e, columns 16*wave + 4q .. +3.
+      u32x2 uraw[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int t0 = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1);
+        const lds_char* up = stage + L::U_OFF + ((t0 + e) * VT + 16 * wave + 4 * q) * 2;
+        uraw[tt] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)up));
+      }
+      // W operands: tile tt row i = n holds token sigma(tt, n); contraction slice 8g..8g+7 of
+      // k-block kb is LDS piece 4kb + g of that row.
+      u32x4 wop[4][KB];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int row = 32 * (tt >> 1) + 8 * e + 4 * (tt & 1) + q;
+        const u32x4* wrow = (const u32x4*)(sbase + L::W_OFF) + row * P;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) wop[tt][kb] = wrow[(4 * kb + g) ^ swz_w<P>(row)];
+      }
+      // bf16(-S): the MM1 B operands (so MM1 accumulates U - W S onto U) and the h snapshot,
+      // staged sign-flipped (the store wave flips it back).
       u32x4 Sw[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        Sw[kb][0] = pack_bf16x2(S[2 * kb][0], S[2 * kb][1]);
-        Sw[kb][1] = pack_bf16x2(S[2 * kb][2], S[2 * kb][3]);
-        Sw[kb][2] = pack_bf16x2(S[2 * kb + 1][0], S[2 * kb + 1][1]);
-        Sw[kb][3] = pack_bf16x2(S[2 * kb + 1][2], S[2 * kb + 1][3]);
-        Sb[kb] = __builtin_bit_cast(bf16x8, Sw[kb]);
+        Sw[kb][0] = pack_bf16x2(-S[2 * kb][0], -S[2 * kb][1]);
+        Sw[kb][1] = pack_bf16x2(-S[2 * kb][2], -S[2 * kb][3]);
+        Sw[kb][2] = pack_bf16x2(-S[2 * kb + 1][0], -S[2 * kb + 1][1]);
+        Sw[kb][3] = pack_bf16x2(-S[2 * kb + 1][2], -S[2 * kb + 1][3]);
       }
       {
         u32x4* ss = (u32x4*)(smem + L::SS_OFF + (c & 1) * L::SS_BYTES);
@@ -311,77 +355,82 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) ss[vrow * P + ((4 * kb + g) ^ swz_s<P>(vrow))] = Sw[kb];
       }
-
-      // MM1: acc[tt] = W_tt bf16(S)
       f32x4 acc[4];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
-        const u32x4* wrow = (const u32x4*)(smem + st * L::STAGE_BYTES + L::W_OFF) + row * P;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const u32x4 wv = wrow[(4 * kb + g) ^ swz_w<P>(row)];
-          acc[tt] = mfma_bf16(__builtin_bit_cast(bf16x8, wv), Sb[kb], acc[tt]);
-        }
-      }
+      for (int tt = 0; tt < 4; ++tt)
+        acc[tt] = f32x4{bf16_lo(uraw[tt][0]), bf16_hi(uraw[tt][0]), bf16_lo(uraw[tt][1]), bf16_hi(uraw[tt][1])};
+      __builtin_amdgcn_sched_barrier(0);
 
-      // Epilogue: Vn = U - acc; v_new staging; Vd = bf16(Vn * gamma).
-      bf16x8 Vd[2];
-      {
-        u32x4* sv = (u32x4*)(smem + L::SV_OFF + (c & 1) * L::SV_BYTES);
-        const int vrow = 16 * wave + n;
+      // Phase 2: MM1 acc[tt] = U_tt + W_tt bf16(-S), four independent chains issued k-block
+      // major, with the state decay S *= a on the VALU and the token-block-0 K^T operand reads
+      // (two transposed reads each: lane (g, i) gets K[32tb + 8g + 4half + (0..3)][pi(kt, i)])
+      // slotted between the MFMAs.
+      auto read_kop = [&](int tb, u32x4* kop) {
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-          float vn[8];
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            // U rows 32tb + 8g + 4hh + (0..3), column 16*wave + n, via a transposed read:
-            // source lane 4e+q addresses row t0+e, columns 16*wave + 4q .. +3.
-            const int e = n >> 2, q = n & 3;
-            const int t0 = 32 * tb + 8 * g + 4 * hh;
-            const lds_char* up = stage + L::U_OFF + ((t0 + e) * VT + 16 * wave + 4 * q) * 2;
-            const i16x4 uv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)up);
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              vn[4 * hh + r] = __uint_as_float(((unsigned)(unsigned short)uv[r]) << 16) - acc[2 * tb + hh][r];
-          }
-          u32x4 pv, pd;
-          const f32x4 g0 = *(const f32x4*)(gam + 32 * tb + 8 * g);
-          const f32x4 g1 = *(const f32x4*)(gam + 32 * tb + 8 * g + 4);
-          const float gm[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            pv[j] = pack_bf16x2(vn[2 * j], vn[2 * j + 1]);
-            pd[j] = pack_bf16x2(vn[2 * j] * gm[2 * j], vn[2 * j + 1] * gm[2 * j + 1]);
-          }
-          sv[vrow * 8 + ((4 * tb + g) ^ swz_v(vrow))] = pv;
-          Vd[tb] = __builtin_bit_cast(bf16x8, pd);
-        }
-      }
-
-      // MM2: S = a S + K^T Vd
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        S[kt] = S[kt] * a;
-        const int kb = kt >> 1, hh = kt & 1;
-        const int e = n >> 2, q = n & 3;
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-          u32x4 ko;
+        for (int kt = 0; kt < KT; ++kt) {
+          const int kb = kt >> 1, hh = kt & 1;
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             const int row = 32 * tb + 8 * g + 4 * half + e;
             const int piece = (4 * kb + q) ^ swz_k<P>(row);
             const lds_char* kp = stage + L::K_OFF + (row * P + piece) * 16 + 8 * hh;
-            const i16x4 kv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)kp);
-            const u32x2 kw = __builtin_bit_cast(u32x2, kv);
-            ko[2 * half] = kw[0];
-            ko[2 * half + 1] = kw[1];
+            const u32x2 kw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)kp));
+            kop[kt][2 * half] = kw[0];
+            kop[kt][2 * half + 1] = kw[1];
           }
-          S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, ko), Vd[tb], S[kt]);
         }
+      };
+      u32x4 kop0[KT], kop1[KT];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+          acc[tt] = mfma_bf16(__builtin_bit_cast(bf16x8, wop[tt][kb]), __builtin_bit_cast(bf16x8, Sw[kb]), acc[tt]);
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) S[kt] = S[kt] * a;
+      read_kop(0, kop0);
+#pragma unroll
+      for (int i = 0; i < 4 * KB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, (2 * KT + 4 * KB - 1) / (4 * KB), 0);   // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, (4 * KT + 4 * KB - 1) / (4 * KB), 0);   // DS read
       }
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Phase 3: epilogue of token block 0 (v_new staging, Vd = bf16(Vn * gamma)).
+      u32x4* sv = (u32x4*)(smem + L::SV_OFF + (c & 1) * L::SV_BYTES);
+      const int vrow = 16 * wave + n;
+      auto epilogue = [&](int tb) -> bf16x8 {
+        u32x4 pv, pd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int hh = j >> 1, r = 2 * (j & 1);
+          const float v0 = acc[2 * tb + hh][r], v1 = acc[2 * tb + hh][r + 1];
+          pv[j] = pack_bf16x2(v0, v1);
+          pd[j] = pack_bf16x2(v0 * gm[tb][hh][r], v1 * gm[tb][hh][r + 1]);
+        }
+        sv[vrow * 8 + ((4 * tb + g) ^ swz_v(vrow))] = pv;
+        return __builtin_bit_cast(bf16x8, pd);
+      };
+      const bf16x8 Vd0 = epilogue(0);
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Phase 4: MM2 of token block 0, with the block-1 K^T reads and epilogue slotted in.
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop0[kt]), Vd0, S[kt]);
+      read_kop(1, kop1);
+      const bf16x8 Vd1 = epilogue(1);
+#pragma unroll
+      for (int i = 0; i < KT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Phase 5: MM2 of token block 1.
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[kt]), Vd1, S[kt]);
       wait_lgkm0();
       block_barrier();   // B_c
     }
@@ -398,8 +447,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
         }
     }
-  } else if (wave == NCW) {
-    // ------------------------------------------------------------------ load wave
+  } else if (wave < NCW + NLW) {
+    // ------------------------------------------------------------------ load waves
+    // The tile DMAs of a chunk are dealt round-robin over the NLW load waves (instruction
+    // i goes to wave i % NLW), so each wave's vmcnt covers only its share and more loads are
+    // in flight per CU; load wave 0 also moves the g row and writes the gate factors.
+    const int lw = wave - NCW;
     const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
     const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
     const __bf16* ubase = (const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
@@ -428,122 +481,153 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const char* wsrc = (const char*)wbase;
     const char* ksrc = (const char*)kbase;
     const char* usrc = (const char*)ubase;
-
-    // Issue the W, K, U tiles and the g row of chunk c into stage st.  Every load is a
-    // direct-to-LDS DMA written as inline asm: the compiler then tracks none of them, and
-    // the explicit in-order vmcnt waits below are the only waits (its own tracking cannot
-    // express more than 63 outstanding loads and would drain the whole pipeline instead).
-    // A partial (last) chunk takes a masked path: rows at or past the sequence end are
-    // zero-filled in LDS instead of loaded (the masked loads with other=0 of the reference).
     const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
     const bool has_g = gbase != nullptr;
     const char* gsrc = has_g ? (const char*)gbase : (const char*)wbase;
     const int64_t sgt = has_g ? p.sg_t * 4 : 0;
-    auto issue = [&](int c, int st) {
-      const int64_t t0 = tk.bos + (int64_t)c * kChunk;
-      const int64_t rem = tk.len - (int64_t)c * kChunk;
-      const int len = rem < kChunk ? (int)rem : kChunk;
-      const uint32_t lbase = lds0 + (uint32_t)(st * L::STAGE_BYTES);
-      char* sbase = smem + st * L::STAGE_BYTES;
-      const char* wchunk = wsrc + t0 * stw;
-      const char* kchunk = ksrc + t0 * stk;
-      const char* uchunk = usrc + t0 * stu;
-      const char* gchunk = gsrc + t0 * sgt;
-      const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
-      if (len == kChunk) {
-#pragma unroll
-        for (int m = 0; m < L::DMA_W; ++m) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
-#pragma unroll
-        for (int m = 0; m < L::DMA_W; ++m) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
-#pragma unroll
-        for (int m = 0; m < L::DMA_U; ++m) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
-      } else {
-#pragma unroll
-        for (int m = 0; m < L::DMA_W; ++m) {
-          if (m * RPI + lrow < len) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
-          else *(u32x4*)(sbase + L::W_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int m = 0; m < L::DMA_W; ++m) {
-          if (m * RPI + lrow < len) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
-          else *(u32x4*)(sbase + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int m = 0; m < L::DMA_U; ++m) {
-          if ((64 * m + lane) / PU < len) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
-          else *(u32x4*)(sbase + L::U_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-      dma_b32(gchunk, goff, lbase + L::GRAW_OFF);
-    };
-    // Gate factors of chunk c into stage st from its raw g row: gamma_t = safe_exp(g_last - g_t)
-    // for t < len, 0 for padded rows, and a = exp(g_last) in slot 64.  No gating: gamma = 1, a = 1.
-    auto gates = [&](int c, int st) {
-      const int64_t rem = tk.len - (int64_t)c * kChunk;
-      const int len = rem < kChunk ? (int)rem : kChunk;
-      float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
-      float gamma, a;
-      if (has_g) {
-        const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
-        const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
-        gamma = lane < len ? safe_exp(glast - gv) : 0.f;
-        a = expf(glast);
-      } else {
-        gamma = lane < len ? 1.f : 0.f;
-        a = 1.f;
-      }
-      gdst[lane] = gamma;
-      if (lane == 0) gdst[64] = a;
-    };
 
-    // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
-    // completes loads in order, so the wait for chunk c+1 is "at most (D-2) full chunks
-    // outstanding" while only full chunks follow it, and vmcnt(0) once the (possibly partial,
-    // hence shorter) last chunk of the sequence is among them (cgdr_schedule.h).
-    constexpr int D = STAGES - 1;
-    constexpr int PER_CHUNK = 2 * L::DMA_W + L::DMA_U + 1;
-    static_assert(D >= 1, "at least one chunk of prefetch");
-    static_assert(D == 1 || (D - 2) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
-    constexpr int STEADY_VM = D >= 2 ? (D - 2) * PER_CHUNK : 0;
+    // One load wave's schedule; LW is its index (compile-time, selects its DMA share).
+    auto run_loader = [&](auto lw_tag) {
+      constexpr int LW = decltype(lw_tag)::value;
+      // Issue this wave's share of the W, K, U tiles (and, on wave 0, the g row) of chunk c
+      // into stage st.  Every load is a direct-to-LDS DMA written as inline asm: the compiler
+      // then tracks none of them, and the explicit in-order vmcnt waits below are the only
+      // waits (its own tracking cannot express more than 63 outstanding loads and would drain
+      // the whole pipeline instead).  A partial (last) chunk takes a masked path: rows at or
+      // past the sequence end are zero-filled in LDS instead of loaded (the masked loads with
+      // other=0 of the reference kernel).
+      auto issue = [&](int c, int st) {
+        const int64_t t0 = tk.bos + (int64_t)c * kChunk;
+        const int64_t rem = tk.len - (int64_t)c * kChunk;
+        const int len = rem < kChunk ? (int)rem : kChunk;
+        const uint32_t lbase = lds0 + (uint32_t)(st * L::STAGE_BYTES);
+        char* sbase = smem + st * L::STAGE_BYTES;
+        const char* wchunk = wsrc + t0 * stw;
+        const char* kchunk = ksrc + t0 * stk;
+        const char* uchunk = usrc + t0 * stu;
+        if (len == kChunk) {
+#pragma unroll
+          for (int m = 0; m < L::DMA_W; ++m)
+            if ((m % NLW) == LW) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
+#pragma unroll
+          for (int m = 0; m < L::DMA_W; ++m)
+            if (((L::DMA_W + m) % NLW) == LW) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
+#pragma unroll
+          for (int m = 0; m < L::DMA_U; ++m)
+            if (((2 * L::DMA_W + m) % NLW) == LW) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
+        } else {
+#pragma unroll
+          for (int m = 0; m < L::DMA_W; ++m) {
+            if ((m % NLW) != LW) continue;
+            if (m * RPI + lrow < len) dma_b128(wchunk, woff[m], lbase + L::W_OFF + 1024 * m);
+            else *(u32x4*)(sbase + L::W_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+          for (int m = 0; m < L::DMA_W; ++m) {
+            if (((L::DMA_W + m) % NLW) != LW) continue;
+            if (m * RPI + lrow < len) dma_b128(kchunk, koff[m], lbase + L::K_OFF + 1024 * m);
+            else *(u32x4*)(sbase + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+          for (int m = 0; m < L::DMA_U; ++m) {
+            if (((2 * L::DMA_W + m) % NLW) != LW) continue;
+            if ((64 * m + lane) / PU < len) dma_b128(uchunk, uoff[m], lbase + L::U_OFF + 1024 * m);
+            else *(u32x4*)(sbase + L::U_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+        if constexpr (LW == 0) {
+          const char* gchunk = gsrc + t0 * sgt;
+          const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
+          dma_b32(gchunk, goff, lbase + L::GRAW_OFF);
+        }
+      };
+      // Gate factors of chunk c into stage st from its raw g row (load wave 0 only):
+      // gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows, and a = exp(g_last)
+      // in slot 64.  No gating: gamma = 1, a = 1.
+      auto gates = [&](int c, int st) {
+        if constexpr (LW == 0) {
+          const int64_t rem = tk.len - (int64_t)c * kChunk;
+          const int len = rem < kChunk ? (int)rem : kChunk;
+          float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
+          float gamma, a;
+          if (has_g) {
+            const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
+            const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
+            gamma = lane < len ? safe_exp(glast - gv) : 0.f;
+            a = expf(glast);
+          } else {
+            gamma = lane < len ? 1.f : 0.f;
+            a = 1.f;
+          }
+          gdst[lane] = gamma;
+          if (lane == 0) gdst[64] = a;
+        }
+      };
 
-    // Prologue: chunks 0 .. D-2 issued, chunk 0 landed and gated, then chunk D-1 issued,
-    // leaving chunks 1 .. D-1 in flight at the top of the loop.
-    if (NC > 0) {
-      if constexpr (D == 1) {
-        issue(0, 0);
-        wait_vm<0>();
-        gates(0, 0);
-      } else {
-        for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
-        if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
-        else wait_vm<0>();
-        gates(0, 0);
-        if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
-      }
-    }
-    wait_lgkm0();
-    block_barrier();   // P
+      // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
+      // completes loads in order, so the wait for chunk c+1 is "at most (D-2) full chunks
+      // outstanding" while only full chunks follow it, and vmcnt(0) once the (possibly
+      // partial, hence shorter) last chunk of the sequence is among them (cgdr_schedule.h).
+      constexpr int D = STAGES - 1;
+      constexpr int PER_CHUNK = L::template dma_per_chunk<LW>();
+      static_assert(D >= 1, "at least one chunk of prefetch");
+      static_assert(D == 1 || (D - 2) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
+      constexpr int STEADY_VM = D >= 2 ? (D - 2) * PER_CHUNK : 0;
 
-    for (int c = 0; c < NC; ++c) {
-      if constexpr (D == 1) {
-        if (c + 1 < NC) {
-          issue(c + 1, (c + 1) % STAGES);
+      // Prologue: chunks 0 .. D-2 issued, chunk 0 landed and gated, then chunk D-1 issued,
+      // leaving chunks 1 .. D-1 in flight at the top of the loop.
+      if (NC > 0) {
+        if constexpr (D == 1) {
+          issue(0, 0);
           wait_vm<0>();
-          gates(c + 1, (c + 1) % STAGES);
-        }
-      } else {
-        if (c + 1 < NC) {
-          if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
+          gates(0, 0);
+        } else {
+          for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
+          if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
           else wait_vm<0>();
-          gates(c + 1, (c + 1) % STAGES);
+          gates(0, 0);
+          if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
         }
-        if (c + D < NC) issue(c + D, (c + D) % STAGES);
       }
       wait_lgkm0();
-      block_barrier();   // B_c
+      block_barrier();   // P
+
+      for (int c = 0; c < NC; ++c) {
+        if constexpr (D == 1) {
+          if (c + 1 < NC) {
+            issue(c + 1, (c + 1) % STAGES);
+            wait_vm<0>();
+            gates(c + 1, (c + 1) % STAGES);
+          }
+        } else {
+          if (c + 1 < NC) {
+            if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
+            else wait_vm<0>();
+            gates(c + 1, (c + 1) % STAGES);
+          }
+          if (c + D < NC) issue(c + D, (c + D) % STAGES);
+        }
+        wait_lgkm0();
+        block_barrier();   // B_c
+      }
+    };
+    if constexpr (NLW == 1) {
+      run_loader(std::integral_constant<int, 0>{});
+    } else if constexpr (NLW == 2) {
+      if (lw == 0) run_loader(std::integral_constant<int, 0>{});
+      else run_loader(std::integral_constant<int, 1>{});
+    } else {
+      static_assert(NLW == 4, "1, 2 or 4 load waves");
+      if (lw == 0) run_loader(std::integral_constant<int, 0>{});
+      else if (lw == 1) run_loader(std::integral_constant<int, 1>{});
+      else if (lw == 2) run_loader(std::integral_constant<int, 2>{});
+      else run_loader(std::integral_constant<int, 3>{});
     }
-  } else {
+  } else if (wave == NCW + NLW) {
     // ------------------------------------------------------------------ store wave
+    // h snapshot and v_new of a chunk, from the LDS staging buffers: each 16-lane block takes
+    // units of (16 rows x 8 value columns); two transposed reads give a lane 8 consecutive
+    // value columns of one row, stored as one 16-byte write.
     const int blk = lane >> 4, i = lane & 15;
     const int e = i >> 2, q = i & 3;
     __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
@@ -552,35 +636,47 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 
     auto store_chunk = [&](int c) {
       const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
-      // h snapshot: units of (16 k rows x 4 value columns) per 16-lane block.
       const char* ss = smem + L::SS_OFF + (c & 1) * L::SS_BYTES;
       __bf16* hdst = hbase + (tk.boh + c) * p.sh_c;
-      constexpr int UNITS_H = (KD / 16) * (VT / 4);
+      constexpr int UNITS_H = (KD / 16) * (VT / 8);
 #pragma unroll
       for (int m = 0; m < UNITS_H / 4; ++m) {
         const int unit = 4 * m + blk;
-        const int k0 = 16 * (unit / (VT / 4)), v0 = 4 * (unit % (VT / 4));
-        const int vrow = v0 + e;
+        const int k0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
         const int kk = k0 + 4 * q;
-        const int piece = (kk >> 3) ^ swz_s<P>(vrow);
-        const lds_char* sp = (const lds_char*)ss + (vrow * P + piece) * 16 + 8 * ((kk >> 2) & 1);
-        const i16x4 hv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp);
-        *(u32x2*)(hdst + (int64_t)(k0 + i) * p.V + v0) = __builtin_bit_cast(u32x2, hv);
+        u32x4 hv;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int vrow = v0 + 4 * half + e;
+          const int piece = (kk >> 3) ^ swz_s<P>(vrow);
+          const lds_char* sp = (const lds_char*)ss + (vrow * P + piece) * 16 + 8 * ((kk >> 2) & 1);
+          const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
+          hv[2 * half] = x[0] ^ 0x80008000u;       // staged as bf16(-S)
+          hv[2 * half + 1] = x[1] ^ 0x80008000u;
+        }
+        *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;
       }
       if (vbase_ptr != nullptr) {
         const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
         __bf16* vdst = vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
-        constexpr int UNITS_V = 4 * (VT / 4);
+        constexpr int UNITS_V = 4 * (VT / 8);
 #pragma unroll
-        for (int m = 0; m < UNITS_V / 4; ++m) {
+        for (int m = 0; m < (UNITS_V + 3) / 4; ++m) {
           const int unit = 4 * m + blk;
-          const int t0 = 16 * (unit / (VT / 4)), v0 = 4 * (unit % (VT / 4));
-          const int vrow = v0 + e;
+          if (UNITS_V % 4 != 0 && unit >= UNITS_V) break;
+          const int t0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
           const int tt = t0 + 4 * q;
-          const int piece = (tt >> 3) ^ swz_v(vrow);
-          const lds_char* sp = (const lds_char*)sv + (vrow * 8 + piece) * 16 + 8 * ((tt >> 2) & 1);
-          const i16x4 vv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp);
-          if (t0 + i < len) *(u32x2*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = __builtin_bit_cast(u32x2, vv);
+          u32x4 vv;
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int vrow = v0 + 4 * half + e;
+            const int piece = (tt >> 3) ^ swz_v(vrow);
+            const lds_char* sp = (const lds_char*)sv + (vrow * 8 + piece) * 16 + 8 * ((tt >> 2) & 1);
+            const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
+            vv[2 * half] = x[0];
+            vv[2 * half + 1] = x[1];
+          }
+          if (t0 + i < len) *(u32x4*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = vv;
         }
       }
     };
@@ -592,6 +688,55 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       block_barrier();   // B_c
     }
     if (NC > 0) store_chunk(NC - 1);
+  } else {
+    // ------------------------------------------------------------------ prefetch wave
+    // L2 prefetch: p.prefetch chunks ahead of the compute waves, the head's K, W and U rows
+    // of a chunk are touched one `seg`-byte segment per lane, the segments shared round-robin
+    // among the head's V-tile workgroups, so the load waves' DMAs of that chunk hit L2 rather
+    // than HBM.  A touch is a 4-byte DMA into a scratch LDS area; nothing waits on it until
+    // exit.  Per-lane segment addresses are fixed at entry; a chunk only adds t0 * row stride.
+    // A partial last chunk is not prefetched (a prefetch is only a hint).
+    constexpr int PF_INSTR = 4;
+    const int pf = p.prefetch;
+    const int nvt = p.n_vtiles;
+    const int seg = ((2 * KD) % 128 == 0 && (2 * p.V) % 128 == 0) ? 128 : ((2 * p.V) % 64 == 0 ? 64 : 32);
+    const int segk = 2 * KD / seg, segv = (int)(2 * p.V / seg);
+    const int segs = 64 * (2 * segk + segv);
+    const char* kpf = (const char*)((const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h);
+    const char* wpf = (const char*)((const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h);
+    const char* upf = (const char*)((const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h);
+    const char* lptr[PF_INSTR];
+    int64_t lstride[PF_INSTR];
+#pragma unroll
+    for (int m = 0; m < PF_INSTR; ++m) {
+      int i = tk.vtile + nvt * (64 * m + lane);
+      i = i < segs ? i : segs - 1;
+      if (i < 64 * segk) {
+        lstride[m] = p.sk_t * 2; lptr[m] = kpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
+      } else if (i < 128 * segk) {
+        i -= 64 * segk;
+        lstride[m] = p.sw_t * 2; lptr[m] = wpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
+      } else {
+        i -= 128 * segk;
+        lstride[m] = p.su_t * 2; lptr[m] = upf + (i / segv) * lstride[m] + (int64_t)seg * (i % segv);
+      }
+    }
+    const int npf = (segs / nvt + 63) / 64 < PF_INSTR ? (segs / nvt + 63) / 64 : PF_INSTR;
+    const uint32_t trash = (uint32_t)(uintptr_t)((lds_char*)smem) + L::TRASH_OFF;
+    auto prefetch = [&](int j) {
+      if (pf <= 0 || j >= NC || tk.len - (int64_t)j * kChunk < kChunk) return;
+      const int64_t t0 = tk.bos + (int64_t)j * kChunk;
+#pragma unroll
+      for (int m = 0; m < PF_INSTR; ++m)
+        if (m < npf) dma_b32_addr(lptr[m] + t0 * lstride[m], trash);
+    };
+    for (int j = 1; j < pf; ++j) prefetch(j);
+    block_barrier();   // P
+    for (int c = 0; c < NC; ++c) {
+      prefetch(c + pf);
+      block_barrier();   // B_c
+    }
+    wait_vm<0>();   // the prefetch DMAs write this workgroup's LDS: drain them before exit
   }
 }
 
