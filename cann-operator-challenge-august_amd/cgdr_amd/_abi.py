@@ -163,8 +163,11 @@ def get_plan(args: FwdHArgs) -> FwdHPlan:
     return plan
 
 
-def launch(args: FwdHArgs, stream: int) -> None:
-    check(load().cgdr_fwd_h_launch(ctypes.byref(args), None, 0, ctypes.c_void_p(stream)))
+def launch(args: FwdHArgs, stream: int, workspace: int = 0, workspace_bytes: int = 0) -> None:
+    """Enqueue on `stream`; `workspace` is a device pointer of workspace_size(args) bytes
+    that stays untouched by the caller until the launch has completed on that stream."""
+    check(load().cgdr_fwd_h_launch(ctypes.byref(args), ctypes.c_void_p(workspace or None),
+                                   ctypes.c_size_t(workspace_bytes), ctypes.c_void_p(stream)))
 
 
 def prepare_chunk_offsets(cu_seqlens: list[int], chunk_size: int = CHUNK_SIZE) -> list[int]:

@@ -98,7 +98,10 @@ def _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V
             getattr(a, name)[:] = list(vals)
     if T == 0:
         return
-    _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream)
+    nws = _abi.workspace_size(a)
+    ws = torch.empty(nws, dtype=torch.uint8, device=k.device) if nws > 0 else None
+    _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream,
+                0 if ws is None else ws.data_ptr(), nws)
 
 
 def _check_common(k, w, u, g, initial_state, chunk_size):

@@ -329,6 +329,20 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
   }
 }
 
+// Workspace: the head-major copy of g, needed when g's token stride is not 1 (the kernels
+// read one chunk's g row of one head as one contiguous 256-byte row).
+size_t g_relayout_bytes(const cgdr_fwd_h_args* a) {
+  if (a->g == nullptr || a->stride_g[1] == 1) return 0;
+  return (size_t)a->B * (size_t)a->H * (size_t)a->T * sizeof(float);
+}
+
+hipError_t launch_g_relayout(const cgdr_fwd_h_args* a, float* gt, hipStream_t s) {
+  const dim3 grid((unsigned)((a->T + 63) / 64), (unsigned)((a->H + 63) / 64), (unsigned)a->B);
+  hipLaunchKernelGGL(cgdr::cgdr_g_head_major_kernel, grid, dim3(256), 0, s, a->g, gt, a->T, a->H,
+                     a->stride_g[0], a->stride_g[1], a->stride_g[2]);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -353,7 +367,7 @@ cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* works
   Plan pl;
   cgdr_status st = make_plan(args, &pl);
   if (st != CGDR_OK) return st;
-  *workspace_bytes = 0;
+  *workspace_bytes = g_relayout_bytes(args);
   return CGDR_OK;
 }
 
@@ -373,14 +387,25 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
 }
 
 cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   Plan pl;
   cgdr_status st = make_plan(args, &pl);
   if (st != CGDR_OK) return st;
-  const cgdr::FwdHParams p = to_params(args, pl);
+  cgdr::FwdHParams p = to_params(args, pl);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = hipSuccess;
+  const size_t need = g_relayout_bytes(args);
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(CGDR_ERR_INVALID, "workspace of %zu bytes required (got %zu)", need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(CGDR_ERR_INVALID, "workspace must be 16-byte aligned");
+    e = launch_g_relayout(args, (float*)workspace, s);
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "g relayout launch failed: %s", hipGetErrorString(e));
+    p.g = (const float*)workspace;
+    p.sg_b = args->H * args->T;
+    p.sg_t = 1;
+    p.sg_h = args->T;
+  }
   if (pl.kernel == 0) {
     switch (args->K) {
       case 32: e = dispatch_bf16<32>(p, pl, s); break;

@@ -22,10 +22,12 @@
 //
 // Roles inside a workgroup (wave index):
 //   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
-//   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles and the g row of
-//               chunk c+STAGES-1 (shared round-robin), gate factors of chunk c+1 into LDS
+//   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
+//               c+STAGES-1 (shared round-robin); wave 0 also moves the g row one chunk
+//               further ahead
 //   NCW+NLW     store wave: h snapshot and v_new of chunk c-1 from LDS staging to HBM
-//   NCW+NLW+1   prefetch wave: touches chunk c+prefetch into L2
+//   NCW+NLW+1   gate/prefetch wave: gate factors of chunk c+1 into LDS, and touches chunk
+//               c+prefetch into L2
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
 #pragma once
@@ -282,6 +284,28 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   const int NC = tk.nc;
   const int vbase = tk.vtile * VT;
   const int hk = tk.head / p.head_ratio;
+  const bool has_g = p.g != nullptr;
+
+  // Gate factors of chunk c into stage st from its raw g row (one wave):
+  // gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows, and a = exp(g_last) in
+  // slot 64.  No gating: gamma = 1, a = 1.
+  auto gates = [&](int c, int st) {
+    const int64_t rem = tk.len - (int64_t)c * kChunk;
+    const int len = rem < kChunk ? (int)rem : kChunk;
+    float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
+    float gamma, a;
+    if (has_g) {
+      const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
+      const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
+      gamma = lane < len ? safe_exp(glast - gv) : 0.f;
+      a = expf(glast);
+    } else {
+      gamma = lane < len ? 1.f : 0.f;
+      a = 1.f;
+    }
+    gdst[lane] = gamma;
+    if (lane == 0) gdst[64] = a;
+  };
 
   if (wave < NCW) {
     // ------------------------------------------------------------------ compute wave
@@ -451,7 +475,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     // ------------------------------------------------------------------ load waves
     // The tile DMAs of a chunk are dealt round-robin over the NLW load waves (instruction
     // i goes to wave i % NLW), so each wave's vmcnt covers only its share and more loads are
-    // in flight per CU; load wave 0 also moves the g row and writes the gate factors.
+    // in flight per CU.  Load wave 0 also moves the raw g row of the NEXT chunk ahead of each
+    // chunk's tiles, so that the row of chunk c+2 has landed when chunk c+1 has, and the
+    // gate wave can turn it into gate factors during chunk c+1 without waiting on anything.
     const int lw = wave - NCW;
     const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
     const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
@@ -482,18 +508,27 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const char* ksrc = (const char*)kbase;
     const char* usrc = (const char*)ubase;
     const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
-    const bool has_g = gbase != nullptr;
     const char* gsrc = has_g ? (const char*)gbase : (const char*)wbase;
     const int64_t sgt = has_g ? p.sg_t * 4 : 0;
 
     // One load wave's schedule; LW is its index (compile-time, selects its DMA share).
     auto run_loader = [&](auto lw_tag) {
       constexpr int LW = decltype(lw_tag)::value;
-      // Issue this wave's share of the W, K, U tiles (and, on wave 0, the g row) of chunk c
-      // into stage st.  Every load is a direct-to-LDS DMA written as inline asm: the compiler
-      // then tracks none of them, and the explicit in-order vmcnt waits below are the only
-      // waits (its own tracking cannot express more than 63 outstanding loads and would drain
-      // the whole pipeline instead).  A partial (last) chunk takes a masked path: rows at or
+      // Raw g row of chunk j (wave 0) into the GRAW area of its stage; rows past the
+      // sequence end repeat the last row.  Without g the same instruction moves filler, so
+      // every chunk issues the same number of loads.
+      auto issue_g = [&](int j) {
+        const int64_t rem = tk.len - (int64_t)j * kChunk;
+        const int len = rem < kChunk ? (int)rem : kChunk;
+        const char* gchunk = gsrc + (tk.bos + (int64_t)j * kChunk) * sgt;
+        const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
+        dma_b32(gchunk, goff, lds0 + (uint32_t)((j % STAGES) * L::STAGE_BYTES + L::GRAW_OFF));
+      };
+      // Issue this wave's share of the W, K, U tiles of chunk c into stage st (on wave 0,
+      // preceded by the g row of chunk c+1).  Every load is a direct-to-LDS DMA written as
+      // inline asm: the compiler then tracks none of them, and the explicit in-order vmcnt
+      // waits below are the only waits (its own tracking cannot express more than 63
+      // outstanding loads and would drain the whole pipeline instead).  A partial (last) chunk takes a masked path: rows at or
       // past the sequence end are zero-filled in LDS instead of loaded (the masked loads with
       // other=0 of the reference kernel).
       auto issue = [&](int c, int st) {
@@ -505,6 +540,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         const char* wchunk = wsrc + t0 * stw;
         const char* kchunk = ksrc + t0 * stk;
         const char* uchunk = usrc + t0 * stu;
+        if constexpr (LW == 0) {
+          if (c + 1 < NC) issue_g(c + 1);
+        }
         if (len == kChunk) {
 #pragma unroll
           for (int m = 0; m < L::DMA_W; ++m)
@@ -535,33 +573,6 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             else *(u32x4*)(sbase + L::U_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
           }
         }
-        if constexpr (LW == 0) {
-          const char* gchunk = gsrc + t0 * sgt;
-          const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
-          dma_b32(gchunk, goff, lbase + L::GRAW_OFF);
-        }
-      };
-      // Gate factors of chunk c into stage st from its raw g row (load wave 0 only):
-      // gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows, and a = exp(g_last)
-      // in slot 64.  No gating: gamma = 1, a = 1.
-      auto gates = [&](int c, int st) {
-        if constexpr (LW == 0) {
-          const int64_t rem = tk.len - (int64_t)c * kChunk;
-          const int len = rem < kChunk ? (int)rem : kChunk;
-          float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
-          float gamma, a;
-          if (has_g) {
-            const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
-            const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
-            gamma = lane < len ? safe_exp(glast - gv) : 0.f;
-            a = expf(glast);
-          } else {
-            gamma = lane < len ? 1.f : 0.f;
-            a = 1.f;
-          }
-          gdst[lane] = gamma;
-          if (lane == 0) gdst[64] = a;
-        }
       };
 
       // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
@@ -574,18 +585,21 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       static_assert(D == 1 || (D - 2) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
       constexpr int STEADY_VM = D >= 2 ? (D - 2) * PER_CHUNK : 0;
 
-      // Prologue: chunks 0 .. D-2 issued, chunk 0 landed and gated, then chunk D-1 issued,
-      // leaving chunks 1 .. D-1 in flight at the top of the loop.
+      // Prologue: g row 0, then chunks 0 .. D-2 issued, chunk 0 (with g rows 0 and 1)
+      // landed and gated here, then chunk D-1 issued, leaving chunks 1 .. D-1 in flight at
+      // the top of the loop.  The gate wave gates chunk c+1 during loop iteration c.
       if (NC > 0) {
+        if constexpr (LW == 0) issue_g(0);
         if constexpr (D == 1) {
           issue(0, 0);
           wait_vm<0>();
-          gates(0, 0);
         } else {
           for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
           if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
           else wait_vm<0>();
-          gates(0, 0);
+        }
+        if constexpr (LW == 0) gates(0, 0);
+        if constexpr (D >= 2) {
           if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
         }
       }
@@ -597,17 +611,15 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           if (c + 1 < NC) {
             issue(c + 1, (c + 1) % STAGES);
             wait_vm<0>();
-            gates(c + 1, (c + 1) % STAGES);
           }
         } else {
           if (c + 1 < NC) {
             if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
             else wait_vm<0>();
-            gates(c + 1, (c + 1) % STAGES);
           }
           if (c + D < NC) issue(c + D, (c + D) % STAGES);
         }
-        wait_lgkm0();
+        wait_lgkm0();      // zero-fill writes of a partial chunk
         block_barrier();   // B_c
       }
     };
@@ -689,7 +701,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
     if (NC > 0) store_chunk(NC - 1);
   } else {
-    // ------------------------------------------------------------------ prefetch wave
+    // ------------------------------------------------------------------ gate/prefetch wave
+    // Gate factors of chunk c+1 during iteration c: its raw g row landed with chunk c+1's
+    // tiles, before barrier B_{c-1}, and the factors are read after barrier B_c.
     // L2 prefetch: p.prefetch chunks ahead of the compute waves, the head's K, W and U rows
     // of a chunk are touched one `seg`-byte segment per lane, the segments shared round-robin
     // among the head's V-tile workgroups, so the load waves' DMAs of that chunk hit L2 rather
@@ -734,9 +748,32 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     block_barrier();   // P
     for (int c = 0; c < NC; ++c) {
       prefetch(c + pf);
+      if (c + 1 < NC) gates(c + 1, (c + 1) % STAGES);
+      wait_lgkm0();
       block_barrier();   // B_c
     }
     wait_vm<0>();   // the prefetch DMAs write this workgroup's LDS: drain them before exit
+  }
+}
+
+// =============================================================================================
+// g relayout: [B, T, H] (any strides) -> head-major [B, H, T] in the workspace, so that the
+// g row of one chunk of one head is 256 contiguous bytes (4 cache lines) instead of 64 rows of
+// a token-major array (64 cache lines per chunk and workgroup).  One 64-token x 64-head tile
+// per workgroup, transposed through LDS: reads coalesced along heads, writes along tokens.
+__global__ void __launch_bounds__(256)
+cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, int64_t T, int64_t H,
+                         int64_t sg_b, int64_t sg_t, int64_t sg_h) {
+  __shared__ float tile[64][65];
+  const int64_t t0 = (int64_t)blockIdx.x * 64, h0 = (int64_t)blockIdx.y * 64, b = blockIdx.z;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int tt = i >> 6, hh = i & 63;
+    if (t0 + tt < T && h0 + hh < H) tile[tt][hh] = g[b * sg_b + (t0 + tt) * sg_t + (h0 + hh) * sg_h];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int hh = i >> 6, tt = i & 63;
+    if (t0 + tt < T && h0 + hh < H) gt[(b * H + h0 + hh) * T + t0 + tt] = tile[tt][hh];
   }
 }
 

@@ -102,12 +102,14 @@ typedef struct cgdr_fwd_h_args {
 } cgdr_fwd_h_args;
 
 /* Phase 1 (host only, no device access): validate the arguments and report the
- * workspace the launch needs.  This build needs none, so *workspace_bytes is 0 on
- * success.  Replaces aclnnChunkGatedDeltaRuleFwdHGetWorkspaceSize. */
+ * workspace the launch needs: B*H*T*4 bytes (a head-major copy of g) when g is given with a
+ * token stride other than 1, else 0.  Replaces aclnnChunkGatedDeltaRuleFwdHGetWorkspaceSize. */
 cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* workspace_bytes);
 
 /* Phase 2: validate again and enqueue the operator on `stream` (a hipStream_t, or
- * NULL for the default stream).  `workspace` may be NULL when workspace_bytes is 0.
+ * NULL for the default stream).  `workspace` (16-byte aligned device memory of at least
+ * the phase-1 size; NULL when that size is 0) must not be in use by another launch until
+ * this one has completed on `stream`.
  * Replaces aclnnChunkGatedDeltaRuleFwdH(workspace, size, executor, stream) and the
  * kernel launch of the Triton wrapper (docs/problem.txt:475-499). */
 cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace,

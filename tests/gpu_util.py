@@ -69,7 +69,9 @@ def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=
         a.stride_h0[:] = list(h0.stride()[:2])
     if f is not None:
         a.stride_final[:] = list(f.stride()[:2])
-    _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream)
+    nws = _abi.workspace_size(a)
+    ws = torch.full((max(nws, 1),), 0xAB, dtype=torch.uint8, device=k.device)
+    _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream, ws.data_ptr() if nws else 0, nws)
     torch.cuda.synchronize()
     return h, v, f
 

@@ -92,6 +92,32 @@ def test_valid_args_need_no_workspace(lib):
     assert _status(_args(dtype=_abi.CGDR_F32, K=64, V=64))[0] == _abi.CGDR_OK
 
 
+def _with_g(a, token_major=True):
+    a.g = 1 << 24
+    B, T, H = a.B, a.T, a.H
+    a.stride_g[:] = [T * H, H, 1] if token_major else [H * T, 1, T]
+    return a
+
+
+def test_token_major_g_needs_head_major_workspace(lib):
+    # a token-major g is copied head-major into the workspace (B*H*T floats); a head-major g
+    # (token stride 1) is read in place
+    assert _status(_with_g(_args(B=2, T=200, H=4))) == (_abi.CGDR_OK, 2 * 4 * 200 * 4)
+    assert _status(_with_g(_args(B=2, T=200, H=4), token_major=False)) == (_abi.CGDR_OK, 0)
+    assert _status(_with_g(_args(varlen=[0, 61, 64], T=64)))[1] == 4 * 64 * 4
+
+
+def test_launch_rejects_missing_or_short_workspace(lib):
+    # host-side check before anything is enqueued, so it runs without a GPU
+    a = _with_g(_args())
+    need = _status(a)[1]
+    assert lib.cgdr_fwd_h_launch(ctypes.byref(a), None, 0, None) == _abi.CGDR_ERR_INVALID
+    assert "workspace" in _abi.last_error()
+    assert lib.cgdr_fwd_h_launch(ctypes.byref(a), ctypes.c_void_p(1 << 24), need - 4, None) == _abi.CGDR_ERR_INVALID
+    assert lib.cgdr_fwd_h_launch(ctypes.byref(a), ctypes.c_void_p((1 << 24) + 4), need, None) == _abi.CGDR_ERR_INVALID
+    assert "aligned" in _abi.last_error()
+
+
 @pytest.mark.parametrize("mutate,expect", [
     (lambda a: setattr(a, "k", None), _abi.CGDR_ERR_NULLPTR),
     (lambda a: setattr(a, "w", None), _abi.CGDR_ERR_NULLPTR),
