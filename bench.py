@@ -90,7 +90,11 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-heads", type=int, default=8)
+    ap.add_argument("--cpu-sample-heads", type=int, default=32)
+    ap.add_argument("--cpu-repeats", type=int, default=7)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB fp32 elementwise copy (the reference kernel of known "
+                         "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path has no multi-GPU component "
@@ -102,6 +106,15 @@ def main():
     import cgdr_amd
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "torch.mul(src, 1.0, out=dst)", "read_bytes": src.numel() * 4,
+                          "write_bytes": dst.numel() * 4, "launches": 3}), flush=True)
+        return
     W = WORKLOAD
     B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
     NT = (T + 63) // 64
@@ -169,7 +182,7 @@ def main():
                      "algorithmic_bytes": nbytes},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads)
+        out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads, args.cpu_repeats)
         out["cpu_baseline"]["speedup"] = tokens_per_s / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
 
