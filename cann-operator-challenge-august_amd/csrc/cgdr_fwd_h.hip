@@ -30,6 +30,7 @@ cgdr_status fail(cgdr_status st, const char* fmt, ...) {
 constexpr int64_t kMaxHeadDim = 256;     // docs/problem.txt:466 (Triton wrapper assert K <= 256)
 constexpr int64_t kMaxValueDim = 1024;   // V-tiling lifts the reference's K == V <= 256
 constexpr int64_t kMaxTasks = 1 << 30;
+constexpr int64_t kCUs = 256;            // MI355X compute units (one workgroup per CU)
 
 int env_int(const char* name, int dflt) {
   const char* s = getenv(name);
@@ -39,6 +40,7 @@ int env_int(const char* name, int dflt) {
 
 struct Plan {
   int kernel;        // 0 bf16 pipeline, 1 fp32
+  int helpers;       // bf16: one L2-prefetch workgroup per task
   int ncw;           // compute waves (Vt = 16 * ncw)
   int nlw;           // load waves (bf16 pipeline)
   int stages;
@@ -158,12 +160,20 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   }
 
   int ncw;
+  const int64_t pairs = a->N * a->H;
+  // Helper mode (bf16 only): 32-column V-tiles, and one L2-prefetch workgroup beside every
+  // task, when tasks and helpers together fit the chip at one workgroup per CU.
+  const int helpers_env = env_int("CGDR_FWD_H_HELPERS", -1);
+  const bool helper_shape = a->in_dtype == CGDR_BF16 && K <= 128 && V % 32 == 0 &&
+                            (pairs * (V / 32)) % 8 == 0 && 2 * pairs * (V / 32) <= kCUs;
+  const bool use_helpers = helper_shape && helpers_env != 0;
   int forced = env_int("CGDR_FWD_H_VTILE", 0);
   if (forced == 16 || forced == 32 || forced == 64) {
     ncw = forced / 16;
+  } else if (use_helpers) {
+    ncw = 2;
   } else {
     // Enough workgroups to cover the 256 CUs first, then wider V-tiles (fewer K/W re-reads).
-    const int64_t pairs = a->N * a->H;
     ncw = 1;
     if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
   }
@@ -181,7 +191,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
     int nlw = env_int("CGDR_FWD_H_LOADERS", 0);
-    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = 2;
+    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = use_helpers ? 4 : 2;
     pl->nlw = nlw;
     int stages = env_int("CGDR_FWD_H_STAGES", 0);
     // deepest ring that fits the LDS and the vmcnt range
@@ -193,6 +203,12 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   }
   pl->tasks = a->N * a->H * (V / (16 * ncw));
   if (pl->tasks > kMaxTasks) return fail(CGDR_ERR_UNSUPPORTED, "too many tasks (%lld)", (long long)pl->tasks);
+  // Helper workgroups (one per task, on the task's XCD) when the doubled grid still fits the
+  // chip at one workgroup per CU, so that tasks and helpers are all resident together.
+  pl->helpers = 0;
+  if (pl->kernel == 0 && pl->tasks % 8 == 0 && 2 * pl->tasks <= kCUs && helpers_env != 0 &&
+      (use_helpers || helpers_env == 1))
+    pl->helpers = 1;
   return CGDR_OK;
 }
 
@@ -218,13 +234,22 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.final_f32 = a->final_dtype == CGDR_F32;
   p.has_g = a->g != nullptr;
   p.prefetch = env_int("CGDR_FWD_H_PREFETCH", 4);
+  p.helpers = pl.helpers;
+  p.helper_lead = env_int("CGDR_FWD_H_HELPER_LEAD", 8);
+  {
+    int hw = env_int("CGDR_FWD_H_HELPER_WAVES", 4);
+    const int max_hw = pl.threads / 64;
+    p.helper_waves = hw < 1 ? 1 : (hw > max_hw ? max_hw : hw);
+  }
+  p.progress = nullptr;
   return p;
 }
 
 template <int KD, int NCW, int NLW, int STAGES>
 hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
   using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES>), dim3((unsigned)tasks),
+  const unsigned grid = (unsigned)(p.helpers ? 2 * tasks : tasks);
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES>), dim3(grid),
                      dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
@@ -330,10 +355,15 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
 }
 
 // Workspace: the head-major copy of g, needed when g's token stride is not 1 (the kernels
-// read one chunk's g row of one head as one contiguous 256-byte row).
+// read one chunk's g row of one head as one contiguous 256-byte row), then, with helper
+// workgroups, one int32 progress counter per task.
 size_t g_relayout_bytes(const cgdr_fwd_h_args* a) {
   if (a->g == nullptr || a->stride_g[1] == 1) return 0;
-  return (size_t)a->B * (size_t)a->H * (size_t)a->T * sizeof(float);
+  return ((size_t)a->B * (size_t)a->H * (size_t)a->T * sizeof(float) + 255) & ~(size_t)255;
+}
+
+size_t workspace_bytes_of(const cgdr_fwd_h_args* a, const Plan& pl) {
+  return g_relayout_bytes(a) + (pl.helpers ? (size_t)pl.tasks * cgdr::kProgressStride * sizeof(int32_t) : 0);
 }
 
 hipError_t launch_g_relayout(const cgdr_fwd_h_args* a, float* gt, hipStream_t s) {
@@ -367,7 +397,7 @@ cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* works
   Plan pl;
   cgdr_status st = make_plan(args, &pl);
   if (st != CGDR_OK) return st;
-  *workspace_bytes = g_relayout_bytes(args);
+  *workspace_bytes = workspace_bytes_of(args, pl);
   return CGDR_OK;
 }
 
@@ -382,7 +412,7 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
   plan->total_waves = pl.threads / 64;
   plan->stages = pl.stages;
   plan->lds_bytes = lds_bytes_of(pl, args->K);
-  plan->workgroups = pl.tasks;
+  plan->workgroups = pl.helpers ? 2 * pl.tasks : pl.tasks;
   return CGDR_OK;
 }
 
@@ -393,18 +423,28 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
   cgdr::FwdHParams p = to_params(args, pl);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e = hipSuccess;
-  const size_t need = g_relayout_bytes(args);
+  const size_t need = workspace_bytes_of(args, pl);
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need)
       return fail(CGDR_ERR_INVALID, "workspace of %zu bytes required (got %zu)", need,
                   workspace == nullptr ? (size_t)0 : workspace_bytes);
     if (!aligned(workspace, 16)) return fail(CGDR_ERR_INVALID, "workspace must be 16-byte aligned");
+  }
+  const size_t g_bytes = g_relayout_bytes(args);
+  if (g_bytes > 0) {
     e = launch_g_relayout(args, (float*)workspace, s);
     if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "g relayout launch failed: %s", hipGetErrorString(e));
     p.g = (const float*)workspace;
     p.sg_b = args->H * args->T;
     p.sg_t = 1;
     p.sg_h = args->T;
+  }
+  if (pl.helpers) {
+    p.progress = (int32_t*)((char*)workspace + g_bytes);
+    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, p.progress,
+                       (int64_t)pl.tasks * cgdr::kProgressStride);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "progress reset launch failed: %s", hipGetErrorString(e));
   }
   if (pl.kernel == 0) {
     switch (args->K) {

@@ -79,8 +79,24 @@ struct FwdHParams {
   int32_t final_f32;    // final_state dtype is fp32 (else bf16)
   int32_t has_g;
   int32_t prefetch;     // L2 prefetch distance in chunks (0: off)
+  int32_t helpers;      // 1: one L2-prefetch workgroup per task (grid = 2 * n_tasks)
+  int32_t helper_lead;  // chunks a helper runs ahead of its task's load waves
+  int32_t helper_waves; // waves per helper workgroup issuing touches
   int32_t reserved;
+  int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
+                        // task (kProgressStride ints; zeroed before launch)
 };
+
+constexpr int kProgressStride = 32;
+
+// Scalar load that bypasses the scalar cache (reads L2): a helper workgroup polls its task's
+// progress counter with it, so the poll never waits behind the helper's own outstanding
+// vector loads (those are counted by vmcnt, this by lgkmcnt).
+__device__ __forceinline__ int poll_l2(const int* addr) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0 glc\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(addr) : "memory");
+  return v;
+}
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
 __device__ __forceinline__ constexpr int waitcnt_imm(int vm, int lgkm) {
@@ -167,6 +183,15 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
 // Task decoding shared by both kernels.  Workgroups are dealt to the 8 XCDs round-robin
 // (blockIdx % 8), so consecutive task ids are remapped onto one XCD: the V-tiles of a head,
 // and the heads sharing a key head, then share that XCD's L2 for their K and W reads.
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
+template <int I0, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I0 < N) {
+    f(std::integral_constant<int, I0>{});
+    static_for<I0 + 1, N>(f);
+  }
+}
+
 struct Task {
   int n, head, vtile;
   int64_t bos, len, boh;   // token offset, length, first chunk index of the sequence
@@ -276,9 +301,19 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[L::LDS_BYTES];
   static_assert(L::LDS_BYTES <= 160 * 1024, "LDS budget of one gfx950 workgroup exceeded");
 
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
   const int lane = threadIdx.x & 63;
-  const int task_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int slot = xcd_remap(blockIdx.x, gridDim.x);
+  // With helpers the grid is 2 * n_tasks (n_tasks a multiple of 8): every XCD holds m tasks
+  // followed by their m helpers, so a helper and its task share that XCD's L2.
+  int task_id = slot;
+  bool helper = false;
+  if (p.helpers) {
+    const int m = p.n_tasks >> 3;
+    const int x = slot / (2 * m), i = slot - x * 2 * m;
+    helper = i >= m;
+    task_id = x * m + (helper ? i - m : i);
+  }
   if (task_id >= p.n_tasks) return;   // uniform per workgroup
   const Task tk = decode_task(p, task_id);
   const int NC = tk.nc;
@@ -307,6 +342,109 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     if (lane == 0) gdst[64] = a;
   };
 
+  // L2 touch of chunk j: the head's K, W and U rows of the chunk are touched one `seg`-byte
+  // segment per lane (a 4-byte DMA into a scratch LDS area; nothing waits on it until exit),
+  // the segments shared round-robin among the head's V-tile tasks, so that the load waves'
+  // DMAs of that chunk hit L2 rather than HBM.  Per-lane segment addresses are fixed here; a
+  // chunk only adds t0 * row stride.  Used by the gate/prefetch wave (touching a few chunks
+  // ahead of its own load waves) or, in helper mode, by the task's helper workgroup.
+  constexpr int PF_INSTR = 4;
+  const char* lptr[PF_INSTR];
+  int64_t lstride[PF_INSTR];
+  int npf = 0;
+  const uint32_t trash = (uint32_t)(uintptr_t)((lds_char*)smem) + L::TRASH_OFF;
+  auto l2_touch_setup = [&]() {
+    const int nvt = p.n_vtiles;
+    const int seg = ((2 * KD) % 128 == 0 && (2 * p.V) % 128 == 0) ? 128 : ((2 * p.V) % 64 == 0 ? 64 : 32);
+    const int segk = 2 * KD / seg, segv = (int)(2 * p.V / seg);
+    const int segs = 64 * (2 * segk + segv);
+    const char* kpf = (const char*)((const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h);
+    const char* wpf = (const char*)((const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h);
+    const char* upf = (const char*)((const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h);
+#pragma unroll
+    for (int m = 0; m < PF_INSTR; ++m) {
+      int i = tk.vtile + nvt * (64 * m + lane);
+      i = i < segs ? i : segs - 1;
+      if (i < 64 * segk) {
+        lstride[m] = p.sk_t * 2; lptr[m] = kpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
+      } else if (i < 128 * segk) {
+        i -= 64 * segk;
+        lstride[m] = p.sw_t * 2; lptr[m] = wpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
+      } else {
+        i -= 128 * segk;
+        lstride[m] = p.su_t * 2; lptr[m] = upf + (i / segv) * lstride[m] + (int64_t)seg * (i % segv);
+      }
+    }
+    npf = (segs / nvt + 63) / 64 < PF_INSTR ? (segs / nvt + 63) / 64 : PF_INSTR;
+  };
+  auto l2_touch = [&](int j) {
+    const int64_t t0 = tk.bos + (int64_t)j * kChunk;
+#pragma unroll
+    for (int m = 0; m < PF_INSTR; ++m)
+      if (m < npf) dma_b32_addr(lptr[m] + t0 * lstride[m], trash);
+  };
+
+  if (helper) {
+    // ------------------------------------------------------------------ helper workgroup
+    // Takes the task's HBM misses on this CU, so that the task's own CU only sees L2 hits
+    // (an HBM miss holds up every later load of the CU that issued it).  One wave touches
+    // chunks up to `helper_lead` chunks beyond the task's load waves, pacing itself on the
+    // task's progress counter.  Nothing waits on a helper; a helper gives up after a bounded
+    // number of idle polls, so it always exits.
+    const int hwaves = p.helper_waves;
+    if (wave >= hwaves) return;
+    // Helper waves take chunks round-robin (wave w: chunks w+1, w+1+hwaves, ...).
+    // Helper v of the head's n_vtiles covers rows [v R, (v+1) R), R = 64 / n_vtiles, of the
+    // chunk's K, W and U rows (whole rows: every V-tile's U), with 16-byte-per-lane DMAs over
+    // contiguous rows into a 1 KiB scratch area; helper 0 also touches the chunk's g row.
+    const int nvt = p.n_vtiles;
+    const int R = 64 / nvt;
+    const int r0 = tk.vtile * R;
+    const char* hk_base = (const char*)((const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h);
+    const char* hw_base = (const char*)((const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h);
+    const char* hu_base = (const char*)((const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h);
+    const char* hg_base = has_g ? (const char*)(p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h) : nullptr;
+    const int64_t hk_st = p.sk_t * 2, hw_st = p.sw_t * 2, hu_st = p.su_t * 2, hg_st = p.sg_t * 4;
+    const uint32_t hscratch = (uint32_t)(uintptr_t)((lds_char*)smem);
+    auto touch_rows = [&](const char* base, int64_t stride, int row_bytes) {
+      const int lpr = row_bytes / 16;           // lanes per row
+      const int rpi = 64 / lpr;                 // rows per instruction
+      const int lrow = lane / lpr, lcol = lane % lpr;
+      for (int r = r0; r < r0 + R; r += rpi) {
+        const int row = r + lrow;
+        if (row < r0 + R)
+          dma_b128(base, (uint32_t)(row * stride) + 16u * (uint32_t)lcol, hscratch);
+      }
+    };
+    auto helper_touch = [&](int j) {
+      const int64_t t0 = tk.bos + (int64_t)j * kChunk;
+      touch_rows(hk_base + t0 * hk_st, hk_st, 2 * KD);
+      touch_rows(hw_base + t0 * hw_st, hw_st, 2 * KD);
+      touch_rows(hu_base + t0 * hu_st, hu_st, (int)(2 * p.V));
+      if (hg_base != nullptr && tk.vtile == 0) dma_b32(hg_base + t0 * hg_st, (uint32_t)(lane * hg_st), hscratch);
+    };
+    constexpr int D = STAGES - 1;
+    const int* prog_addr = p.progress + task_id * kProgressStride;
+    int issued = 1 + wave;   // chunk 0 is loaded before the task's first barrier
+    int idle = 0;
+    const int max_idle = 8 * NC + 4096;
+    while (issued < NC) {
+      const int done = poll_l2(prog_addr);
+      int target = done + D + p.helper_lead;
+      target = target < NC ? target : NC;
+      if (issued < target) {
+        for (; issued < target; issued += hwaves)
+          if (tk.len - (int64_t)issued * kChunk >= kChunk) helper_touch(issued);
+        idle = 0;
+      } else {
+        if (++idle > max_idle) break;
+        __builtin_amdgcn_s_sleep(16);
+      }
+    }
+    wait_vm<0>();   // the touches write this workgroup's LDS: drain them before exit
+    return;
+  }
+
   if (wave < NCW) {
     // ------------------------------------------------------------------ compute wave
     const int g = lane >> 4, n = lane & 15;
@@ -329,8 +467,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
     block_barrier();   // P: stage 0 ready
 
-    for (int c = 0; c < NC; ++c) {
-      const int st = c % STAGES;
+    // One chunk; the stage (c % STAGES) and the staging buffer (c % 2) are template constants,
+    // so every LDS address below is a fixed offset from a per-lane base (the chunk loop is
+    // unrolled over a whole cycle of both).
+    auto chunk_step = [&](const int c, auto st_tag, auto par_tag) {
+      constexpr int st = decltype(st_tag)::value;
+      constexpr int par = decltype(par_tag)::value;
       const char* sbase = smem + st * L::STAGE_BYTES;
       const lds_char* stage = (const lds_char*)sbase;
       const float* gam = (const float*)(sbase + L::G_OFF);
@@ -374,7 +516,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         Sw[kb][3] = pack_bf16x2(-S[2 * kb + 1][2], -S[2 * kb + 1][3]);
       }
       {
-        u32x4* ss = (u32x4*)(smem + L::SS_OFF + (c & 1) * L::SS_BYTES);
+        u32x4* ss = (u32x4*)(smem + L::SS_OFF + par * L::SS_BYTES);
         const int vrow = 16 * wave + n;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) ss[vrow * P + ((4 * kb + g) ^ swz_s<P>(vrow))] = Sw[kb];
@@ -422,7 +564,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       __builtin_amdgcn_sched_barrier(0);
 
       // Phase 3: epilogue of token block 0 (v_new staging, Vd = bf16(Vn * gamma)).
-      u32x4* sv = (u32x4*)(smem + L::SV_OFF + (c & 1) * L::SV_BYTES);
+      u32x4* sv = (u32x4*)(smem + L::SV_OFF + par * L::SV_BYTES);
       const int vrow = 16 * wave + n;
       auto epilogue = [&](int tb) -> bf16x8 {
         u32x4 pv, pd;
@@ -457,6 +599,14 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[kt]), Vd1, S[kt]);
       wait_lgkm0();
       block_barrier();   // B_c
+    };
+    constexpr int UNROLL = (STAGES % 2 == 0) ? STAGES : 2 * STAGES;
+    for (int c0 = 0; c0 < NC; c0 += UNROLL) {
+      static_for<0, UNROLL>([&](auto i) {
+        constexpr int I = decltype(i)::value;
+        if (c0 + I < NC)
+          chunk_step(c0 + I, std::integral_constant<int, I % STAGES>{}, std::integral_constant<int, I % 2>{});
+      });
     }
 
     if (p.final_state != nullptr) {
@@ -698,52 +848,22 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       if (c >= 1) store_chunk(c - 1);
       wait_lgkm0();
       block_barrier();   // B_c
+      if (p.helpers && lane == 0)
+        __hip_atomic_store(p.progress + task_id * kProgressStride, c + 1, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     if (NC > 0) store_chunk(NC - 1);
-  } else {
+  } else if (wave == NCW + NLW + 1) {
     // ------------------------------------------------------------------ gate/prefetch wave
     // Gate factors of chunk c+1 during iteration c: its raw g row landed with chunk c+1's
     // tiles, before barrier B_{c-1}, and the factors are read after barrier B_c.
-    // L2 prefetch: p.prefetch chunks ahead of the compute waves, the head's K, W and U rows
-    // of a chunk are touched one `seg`-byte segment per lane, the segments shared round-robin
-    // among the head's V-tile workgroups, so the load waves' DMAs of that chunk hit L2 rather
-    // than HBM.  A touch is a 4-byte DMA into a scratch LDS area; nothing waits on it until
-    // exit.  Per-lane segment addresses are fixed at entry; a chunk only adds t0 * row stride.
-    // A partial last chunk is not prefetched (a prefetch is only a hint).
-    constexpr int PF_INSTR = 4;
+    // Without helper workgroups this wave also touches chunk c+prefetch into L2 (l2_touch).
     const int pf = p.prefetch;
-    const int nvt = p.n_vtiles;
-    const int seg = ((2 * KD) % 128 == 0 && (2 * p.V) % 128 == 0) ? 128 : ((2 * p.V) % 64 == 0 ? 64 : 32);
-    const int segk = 2 * KD / seg, segv = (int)(2 * p.V / seg);
-    const int segs = 64 * (2 * segk + segv);
-    const char* kpf = (const char*)((const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h);
-    const char* wpf = (const char*)((const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h);
-    const char* upf = (const char*)((const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h);
-    const char* lptr[PF_INSTR];
-    int64_t lstride[PF_INSTR];
-#pragma unroll
-    for (int m = 0; m < PF_INSTR; ++m) {
-      int i = tk.vtile + nvt * (64 * m + lane);
-      i = i < segs ? i : segs - 1;
-      if (i < 64 * segk) {
-        lstride[m] = p.sk_t * 2; lptr[m] = kpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
-      } else if (i < 128 * segk) {
-        i -= 64 * segk;
-        lstride[m] = p.sw_t * 2; lptr[m] = wpf + (i / segk) * lstride[m] + (int64_t)seg * (i % segk);
-      } else {
-        i -= 128 * segk;
-        lstride[m] = p.su_t * 2; lptr[m] = upf + (i / segv) * lstride[m] + (int64_t)seg * (i % segv);
-      }
-    }
-    const int npf = (segs / nvt + 63) / 64 < PF_INSTR ? (segs / nvt + 63) / 64 : PF_INSTR;
-    const uint32_t trash = (uint32_t)(uintptr_t)((lds_char*)smem) + L::TRASH_OFF;
     auto prefetch = [&](int j) {
-      if (pf <= 0 || j >= NC || tk.len - (int64_t)j * kChunk < kChunk) return;
-      const int64_t t0 = tk.bos + (int64_t)j * kChunk;
-#pragma unroll
-      for (int m = 0; m < PF_INSTR; ++m)
-        if (m < npf) dma_b32_addr(lptr[m] + t0 * lstride[m], trash);
+      if (pf <= 0 || p.helpers || j >= NC || tk.len - (int64_t)j * kChunk < kChunk) return;
+      l2_touch(j);
     };
+    if (pf > 0 && !p.helpers) l2_touch_setup();
     for (int j = 1; j < pf; ++j) prefetch(j);
     block_barrier();   // P
     for (int c = 0; c < NC; ++c) {
@@ -775,6 +895,12 @@ cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, in
     const int hh = i >> 6, tt = i & 63;
     if (t0 + tt < T && h0 + hh < H) gt[(b * H + h0 + hh) * T + t0 + tt] = tile[tt][hh];
   }
+}
+
+// Zero n int32 counters (the helpers' progress counters) ahead of the chunk kernel; a kernel
+// rather than a memset so that the whole call can be captured in a HIP graph.
+__global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __restrict__ x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0;
 }
 
 // =============================================================================================

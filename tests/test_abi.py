@@ -87,9 +87,10 @@ def _status(a):
 
 
 def test_valid_args_need_no_workspace(lib):
-    assert _status(_args()) == (_abi.CGDR_OK, 0)
+    # no g and no helper workgroups (12 tasks: not a multiple of the 8 XCDs)
+    assert _status(_args(H=3, Hg=1)) == (_abi.CGDR_OK, 0)
     assert _status(_args(varlen=[0, 61, 64], T=64))[0] == _abi.CGDR_OK
-    assert _status(_args(dtype=_abi.CGDR_F32, K=64, V=64))[0] == _abi.CGDR_OK
+    assert _status(_args(dtype=_abi.CGDR_F32, K=64, V=64)) == (_abi.CGDR_OK, 0)
 
 
 def _with_g(a, token_major=True):
@@ -102,9 +103,12 @@ def _with_g(a, token_major=True):
 def test_token_major_g_needs_head_major_workspace(lib):
     # a token-major g is copied head-major into the workspace (B*H*T floats); a head-major g
     # (token stride 1) is read in place
-    assert _status(_with_g(_args(B=2, T=200, H=4))) == (_abi.CGDR_OK, 2 * 4 * 200 * 4)
-    assert _status(_with_g(_args(B=2, T=200, H=4), token_major=False)) == (_abi.CGDR_OK, 0)
-    assert _status(_with_g(_args(varlen=[0, 61, 64], T=64)))[1] == 4 * 64 * 4
+    # (3 heads: 12 tasks, no helper workgroups; the copy is rounded up to 256 bytes)
+    assert _status(_with_g(_args(B=1, T=256, H=3, Hg=1))) == (_abi.CGDR_OK, 3 * 256 * 4)
+    assert _status(_with_g(_args(B=1, T=200, H=3, Hg=1))) == (_abi.CGDR_OK, 2560)
+    assert _status(_with_g(_args(B=1, T=200, H=3, Hg=1), token_major=False)) == (_abi.CGDR_OK, 0)
+    # varlen, 2 sequences x 3 heads x 4 V-tiles = 24 tasks: helpers, 24 progress lines
+    assert _status(_with_g(_args(varlen=[0, 61, 64], T=64, H=3, Hg=1)))[1] == 3 * 64 * 4 + 24 * 128
 
 
 def test_launch_rejects_missing_or_short_workspace(lib):
@@ -179,9 +183,24 @@ def test_host_chunk_metadata_rejects_bad_cu(lib):
 
 
 def test_plan_headline_fills_the_chip(lib):
+    # 32 heads x 4 V-tiles of 32 columns, each task with an L2-prefetch helper workgroup on
+    # its XCD: 256 workgroups, one per CU
     p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128))
-    assert p.kernel == 0 and p.v_tile == 16 and p.workgroups == 256
+    assert p.kernel == 0 and p.v_tile == 32 and p.workgroups == 256
     assert p.lds_bytes <= 160 * 1024
+    # helpers need the doubled grid to fit the chip and tasks in multiples of 8 (per XCD)
+    p = _abi.get_plan(_args(B=2, T=4096, H=32, Hg=32, K=128, V=128))
+    assert p.v_tile == 16 and p.workgroups == 2 * 32 * 8
+    p = _abi.get_plan(_args(B=1, T=4096, H=6, Hg=6, K=128, V=128))
+    assert p.workgroups == 6 * 8
+
+
+def test_helper_mode_workspace_holds_progress_counters(lib):
+    # one 128-byte progress line per task, after the (256-byte rounded) head-major g copy
+    a = _args(B=1, T=200, H=32, Hg=32, K=128, V=128)
+    assert _status(a) == (_abi.CGDR_OK, 128 * 128)
+    a = _with_g(_args(B=1, T=200, H=32, Hg=32, K=128, V=128))
+    assert _status(a) == (_abi.CGDR_OK, ((32 * 200 * 4 + 255) // 256) * 256 + 128 * 128)
 
 
 def test_wrapper_refuses_cpu_tensors():

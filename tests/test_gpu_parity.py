@@ -170,6 +170,24 @@ def test_vtile_and_depth_invariance(dev):
                 assert torch.equal(a, b), (key, val)
 
 
+@pytest.mark.parametrize("lens", [None, [100, 61, 239, 64]])
+def test_helper_workgroups_change_nothing(dev, lens):
+    """L2-prefetch helper workgroups only warm L2: outputs are bit-identical with them off, and
+    for any lead (0, the default, or far beyond the sequence) and helper wave count."""
+    if lens is None:
+        inp = _case(61, 1, 700, 8, 128, 128, gate="linear")
+    else:
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        inp = _case(62, 1, int(cu[-1]), 4, 128, 128, shift=4.0, cu=cu, profile="wy")
+    d = dev_inputs(inp, torch.bfloat16, dev)
+    base = _with_env("CGDR_FWD_H_HELPERS", 0, lambda: _with_env("CGDR_FWD_H_VTILE", 32, lambda: abi_call(d)))
+    for key, val in (("CGDR_FWD_H_HELPERS", 1), ("CGDR_FWD_H_HELPER_LEAD", 0),
+                     ("CGDR_FWD_H_HELPER_LEAD", 100000), ("CGDR_FWD_H_HELPER_WAVES", 1)):
+        out = _with_env(key, val, lambda: abi_call(d))
+        for a, b in zip(base, out):
+            assert torch.equal(a, b), (key, val)
+
+
 def test_varlen_equals_separate_sequences(dev):
     lens = [5, 64, 129, 300]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
