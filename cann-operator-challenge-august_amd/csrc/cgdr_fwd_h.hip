@@ -191,14 +191,17 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
     int nlw = env_int("CGDR_FWD_H_LOADERS", 0);
-    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = use_helpers ? 4 : 2;
+    // With helper workgroups the task's loads are L2 hits and one load wave keeps up; at most
+    // 8 waves per workgroup (two per SIMD), so that no wave is squeezed below 256 VGPRs.
+    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = use_helpers ? 1 : 2;
+    while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
     pl->nlw = nlw;
     int stages = env_int("CGDR_FWD_H_STAGES", 0);
     // deepest ring that fits the LDS and the vmcnt range
     const int max_stages = bf16_max_stages(K, ncw, nlw);
     if (stages < 2 || stages > max_stages) stages = max_stages;
     pl->stages = stages;
-    pl->threads = 64 * (ncw + nlw + 2);
+    pl->threads = 64 * (ncw + nlw + ncw + 1);   // compute, load, store (one per compute), gate
     pl->lds = 0;
   }
   pl->tasks = a->N * a->H * (V / (16 * ncw));

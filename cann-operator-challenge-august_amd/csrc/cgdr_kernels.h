@@ -25,8 +25,9 @@
 //   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
 //               c+STAGES-1 (shared round-robin); wave 0 also moves the g row one chunk
 //               further ahead
-//   NCW+NLW     store wave: h snapshot and v_new of chunk c-1 from LDS staging to HBM
-//   NCW+NLW+1   gate/prefetch wave: gate factors of chunk c+1 into LDS, and touches chunk
+//   NCW+NLW .. NCW+NLW+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1
+//               from LDS staging to HBM, store instructions shared round-robin
+//   NCW+NLW+NSW gate/prefetch wave: gate factors of chunk c+1 into LDS, and touches chunk
 //               c+prefetch into L2
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
@@ -265,7 +266,8 @@ struct Bf16Layout {
   static constexpr int SV_BYTES = VT * kChunk * 2;
   static constexpr int TRASH_OFF = SV_OFF + 2 * SV_BYTES;      // L2-prefetch landing area
   static constexpr int LDS_BYTES = TRASH_OFF + 256;
-  static constexpr int THREADS = 64 * (NCW + NLW + 2);
+  static constexpr int NSW = NCW;                              // store waves
+  static constexpr int THREADS = 64 * (NCW + NLW + NSW + 1);
   static constexpr int DMA_W = 128 * KD / 1024;               // DMA instructions per tile
   static constexpr int DMA_U = (128 * VT + 1023) / 1024;
   static constexpr int DMA_TILES = 2 * DMA_W + DMA_U;         // per chunk, over all load waves
@@ -284,7 +286,7 @@ template <int KD, int NCW, int NLW, int STAGES>
 constexpr bool bf16_config_ok() {
   using L = Bf16Layout<KD, NCW, NLW, STAGES>;
   constexpr int per_chunk = L::template dma_per_chunk<0>();
-  return STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES == 2 || (STAGES - 3) * per_chunk <= 63);
+  return STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES - 2) * per_chunk <= 63;
 }
 template <int KD, int NCW, int NLW>
 constexpr int bf16_max_stages() {
@@ -292,7 +294,7 @@ constexpr int bf16_max_stages() {
 }
 
 template <int KD, int NCW, int NLW, int STAGES>
-__global__ void __launch_bounds__(64 * (NCW + NLW + 2))
+__global__ void __launch_bounds__(64 * (NCW + NLW + NCW + 1))
 cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   using L = Bf16Layout<KD, NCW, NLW, STAGES>;
   constexpr int VT = L::VT, P = L::P;
@@ -725,49 +727,34 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       };
 
-      // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  vmcnt
-      // completes loads in order, so the wait for chunk c+1 is "at most (D-2) full chunks
-      // outstanding" while only full chunks follow it, and vmcnt(0) once the (possibly
-      // partial, hence shorter) last chunk of the sequence is among them (cgdr_schedule.h).
+      // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  Each loop
+      // iteration first issues chunk c+D (into the stage the last barrier freed), then waits
+      // for chunk c+1.  vmcnt completes loads in order, so that wait is "at most D-1 full
+      // chunk groups outstanding" while only full groups follow chunk c+1, and vmcnt(0) once
+      // the (possibly shorter) last group of the sequence is among them (cgdr_schedule.h).
       constexpr int D = STAGES - 1;
       constexpr int PER_CHUNK = L::template dma_per_chunk<LW>();
       static_assert(D >= 1, "at least one chunk of prefetch");
-      static_assert(D == 1 || (D - 2) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
-      constexpr int STEADY_VM = D >= 2 ? (D - 2) * PER_CHUNK : 0;
+      static_assert((D - 1) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
+      constexpr int STEADY_VM = (D - 1) * PER_CHUNK;
 
-      // Prologue: g row 0, then chunks 0 .. D-2 issued, chunk 0 (with g rows 0 and 1)
-      // landed and gated here, then chunk D-1 issued, leaving chunks 1 .. D-1 in flight at
-      // the top of the loop.  The gate wave gates chunk c+1 during loop iteration c.
+      // Prologue: g row 0, then chunks 0 .. D-1 issued; chunk 0 (with g rows 0 and 1) landed
+      // and gated here.  The gate wave gates chunk c+1 during loop iteration c.
       if (NC > 0) {
         if constexpr (LW == 0) issue_g(0);
-        if constexpr (D == 1) {
-          issue(0, 0);
-          wait_vm<0>();
-        } else {
-          for (int j = 0; j < D - 1 && j < NC; ++j) issue(j, j);
-          if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
-          else wait_vm<0>();
-        }
+        for (int j = 0; j < D && j < NC; ++j) issue(j, j);
+        if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
+        else wait_vm<0>();
         if constexpr (LW == 0) gates(0, 0);
-        if constexpr (D >= 2) {
-          if (D - 1 < NC) issue(D - 1, (D - 1) % STAGES);
-        }
       }
       wait_lgkm0();
       block_barrier();   // P
 
       for (int c = 0; c < NC; ++c) {
-        if constexpr (D == 1) {
-          if (c + 1 < NC) {
-            issue(c + 1, (c + 1) % STAGES);
-            wait_vm<0>();
-          }
-        } else {
-          if (c + 1 < NC) {
-            if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
-            else wait_vm<0>();
-          }
-          if (c + D < NC) issue(c + D, (c + D) % STAGES);
+        if (c + D < NC) issue(c + D, (c + D) % STAGES);
+        if (c + 1 < NC) {
+          if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
+          else wait_vm<0>();
         }
         wait_lgkm0();      // zero-fill writes of a partial chunk
         block_barrier();   // B_c
@@ -785,11 +772,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       else if (lw == 2) run_loader(std::integral_constant<int, 2>{});
       else run_loader(std::integral_constant<int, 3>{});
     }
-  } else if (wave == NCW + NLW) {
-    // ------------------------------------------------------------------ store wave
+  } else if (wave < NCW + NLW + L::NSW) {
+    // ------------------------------------------------------------------ store waves
     // h snapshot and v_new of a chunk, from the LDS staging buffers: each 16-lane block takes
     // units of (16 rows x 8 value columns); two transposed reads give a lane 8 consecutive
     // value columns of one row, stored as one 16-byte write.
+    const int sw = wave - NCW - NLW;   // this store wave takes store instructions m % NSW == sw
     const int blk = lane >> 4, i = lane & 15;
     const int e = i >> 2, q = i & 3;
     __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
@@ -803,6 +791,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       constexpr int UNITS_H = (KD / 16) * (VT / 8);
 #pragma unroll
       for (int m = 0; m < UNITS_H / 4; ++m) {
+        if (m % L::NSW != sw) continue;
         const int unit = 4 * m + blk;
         const int k0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
         const int kk = k0 + 4 * q;
@@ -824,6 +813,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         constexpr int UNITS_V = 4 * (VT / 8);
 #pragma unroll
         for (int m = 0; m < (UNITS_V + 3) / 4; ++m) {
+          if ((UNITS_H / 4 + m) % L::NSW != sw) continue;
           const int unit = 4 * m + blk;
           if (UNITS_V % 4 != 0 && unit >= UNITS_V) break;
           const int t0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
@@ -848,12 +838,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       if (c >= 1) store_chunk(c - 1);
       wait_lgkm0();
       block_barrier();   // B_c
-      if (p.helpers && lane == 0)
+      if (p.helpers && sw == 0 && lane == 0)
         __hip_atomic_store(p.progress + task_id * kProgressStride, c + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
     if (NC > 0) store_chunk(NC - 1);
-  } else if (wave == NCW + NLW + 1) {
+  } else if (wave == NCW + NLW + L::NSW) {
     // ------------------------------------------------------------------ gate/prefetch wave
     // Gate factors of chunk c+1 during iteration c: its raw g row landed with chunk c+1's
     // tiles, before barrier B_{c-1}, and the factors are read after barrier B_c.
