@@ -1,4 +1,5 @@
-"""Build the in-tree HIP library ``lib/libcgdr_fwd_h.so`` for gfx950.
+"""Build the in-tree HIP library ``lib/libcgdr_fwd_h.so`` for gfx950 and the golden-case
+runner ``lib/cgdr_golden_runner`` (host C++ linked against the library and the HIP runtime).
 
 ``python -m cgdr_amd.build`` (with ``cann-operator-challenge-august_amd`` on sys.path), or
 ``build_library()`` from Python.  hipcc cross-compiles without a GPU.
@@ -15,6 +16,8 @@ REPO_ROOT = os.path.dirname(_PKG_ROOT)
 CSRC = os.path.join(_PKG_ROOT, "csrc")
 LIB_DIR = os.path.join(_PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libcgdr_fwd_h.so")
+RUNNER_PATH = os.path.join(LIB_DIR, "cgdr_golden_runner")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -32,6 +35,7 @@ HIP_FLAGS = [
 ]
 
 SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip")]
+RUNNER_SOURCE = os.path.join(CSRC, "cgdr_golden_runner.cpp")
 HEADERS = [os.path.join(CSRC, "cgdr_kernels.h"), os.path.join(CSRC, "cgdr_schedule.h"), os.path.join(REPO_ROOT, "include", "cgdr_fwd_h.h")]
 
 
@@ -53,5 +57,30 @@ def build_library(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+def build_runner(verbose: bool = False) -> str:
+    """Compile the golden-case runner (host code only) against the built library."""
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} missing: build_library() first")
+    tmp = RUNNER_PATH + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(REPO_ROOT, "include"), "-I", os.path.join(ROCM, "include"),
+           RUNNER_SOURCE, "-o", tmp, "-L", LIB_DIR, "-lcgdr_fwd_h",
+           "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed ({res.returncode}):\n{res.stderr}")
+    if verbose and res.stderr.strip():
+        print(res.stderr, file=sys.stderr)
+    os.replace(tmp, RUNNER_PATH)
+    return RUNNER_PATH
+
+
+def build_all(verbose: bool = False) -> list[str]:
+    return [build_library(verbose), build_runner(verbose)]
+
+
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    print("\n".join(build_all(verbose=True)))

@@ -102,8 +102,10 @@ typedef struct cgdr_fwd_h_args {
 } cgdr_fwd_h_args;
 
 /* Phase 1 (host only, no device access): validate the arguments and report the
- * workspace the launch needs: B*H*T*4 bytes (a head-major copy of g) when g is given with a
- * token stride other than 1, else 0.  Replaces aclnnChunkGatedDeltaRuleFwdHGetWorkspaceSize. */
+ * workspace the launch needs: B*H*T*4 bytes rounded up to 256 (a head-major copy of g) when
+ * g is given with a token stride other than 1, plus 128 bytes per task (progress counters)
+ * when the plan uses helper workgroups; 0 when neither applies.
+ * Replaces aclnnChunkGatedDeltaRuleFwdHGetWorkspaceSize. */
 cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* workspace_bytes);
 
 /* Phase 2: validate again and enqueue the operator on `stream` (a hipStream_t, or
