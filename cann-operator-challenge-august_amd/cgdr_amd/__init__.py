@@ -1,10 +1,12 @@
 """MI355X (gfx950) ChunkGatedDeltaRuleFwdH: the chunked gated delta-rule state recurrence.
 
 Drop-in for the reference's FwdH operator path; see ``fwd_h`` for the two Python
-signatures and ``include/cgdr_fwd_h.h`` for the C ABI they call.
+signatures and ``include/cgdr_fwd_h.h`` for the C ABI they call.  ``chunk_o`` is the
+chunk output built on FwdH's h and v_new (``include/cgdr_chunk_o.h``).
 """
 
 from .fwd_h import CHUNK_SIZE, chunk_gated_delta_rule_fwd_h, plan, run
+from .chunk_o import chunk_fwd_o
 from . import _abi
 
 prepare_chunk_offsets = _abi.prepare_chunk_offsets
@@ -13,6 +15,7 @@ prepare_chunk_indices = _abi.prepare_chunk_indices
 __all__ = [
     "CHUNK_SIZE",
     "chunk_gated_delta_rule_fwd_h",
+    "chunk_fwd_o",
     "run",
     "plan",
     "prepare_chunk_offsets",

@@ -1,4 +1,4 @@
-"""ctypes binding of the C ABI declared in ``include/cgdr_fwd_h.h``.
+"""ctypes binding of the C ABI declared in ``include/cgdr_fwd_h.h`` and ``include/cgdr_chunk_o.h``.
 
 The shared library ``libcgdr_fwd_h.so`` is built in-tree by ``cgdr_amd.build`` into
 ``<package root>/lib``.  Loading it does not touch the GPU; only ``cgdr_fwd_h_launch``
@@ -31,6 +31,8 @@ EXPORTED_SYMBOLS = (
     "cgdr_status_string",
     "cgdr_last_error",
     "cgdr_abi_version",
+    "cgdr_chunk_o_launch",
+    "cgdr_chunk_o_get_plan",
 )
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -92,6 +94,38 @@ class FwdHPlan(ctypes.Structure):
     ]
 
 
+class ChunkOArgs(ctypes.Structure):
+    """Mirror of ``cgdr_chunk_o_args``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v_new", ctypes.c_void_p),
+        ("h", ctypes.c_void_p),
+        ("g", ctypes.c_void_p),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("chunk_indices", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("T", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("Hg", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("V", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("NT", ctypes.c_int64),
+        ("chunk_size", ctypes.c_int64),
+        ("scale", ctypes.c_float),
+        ("in_dtype", ctypes.c_int32),
+        ("stride_q", ctypes.c_int64 * 3),
+        ("stride_k", ctypes.c_int64 * 3),
+        ("stride_v", ctypes.c_int64 * 3),
+        ("stride_h", ctypes.c_int64 * 3),
+        ("stride_g", ctypes.c_int64 * 3),
+        ("stride_o", ctypes.c_int64 * 3),
+    ]
+
+
 class CgdrError(RuntimeError):
     """A non-zero ``cgdr_status`` from the library, with its message."""
 
@@ -129,6 +163,11 @@ def load(path: str | None = None):
     lib.cgdr_status_string.restype = ctypes.c_char_p
     lib.cgdr_last_error.argtypes = []
     lib.cgdr_last_error.restype = ctypes.c_char_p
+    lib.cgdr_chunk_o_launch.argtypes = [ctypes.POINTER(ChunkOArgs), ctypes.c_void_p]
+    lib.cgdr_chunk_o_launch.restype = ctypes.c_int
+    lib.cgdr_chunk_o_get_plan.argtypes = [ctypes.POINTER(ChunkOArgs), ctypes.POINTER(ctypes.c_int32),
+                                          ctypes.POINTER(ctypes.c_int64)]
+    lib.cgdr_chunk_o_get_plan.restype = ctypes.c_int
     lib.cgdr_abi_version.argtypes = []
     lib.cgdr_abi_version.restype = ctypes.c_int
     if lib.cgdr_abi_version() != ABI_VERSION:
@@ -168,6 +207,17 @@ def launch(args: FwdHArgs, stream: int, workspace: int = 0, workspace_bytes: int
     that stays untouched by the caller until the launch has completed on that stream."""
     check(load().cgdr_fwd_h_launch(ctypes.byref(args), ctypes.c_void_p(workspace or None),
                                    ctypes.c_size_t(workspace_bytes), ctypes.c_void_p(stream)))
+
+
+def chunk_o_launch(args: ChunkOArgs, stream: int) -> None:
+    check(load().cgdr_chunk_o_launch(ctypes.byref(args), ctypes.c_void_p(stream)))
+
+
+def chunk_o_plan(args: ChunkOArgs) -> tuple[int, int]:
+    """(v_tile, workgroups) of the launch for ``args``."""
+    vt, wg = ctypes.c_int32(0), ctypes.c_int64(0)
+    check(load().cgdr_chunk_o_get_plan(ctypes.byref(args), ctypes.byref(vt), ctypes.byref(wg)))
+    return vt.value, wg.value
 
 
 def prepare_chunk_offsets(cu_seqlens: list[int], chunk_size: int = CHUNK_SIZE) -> list[int]:

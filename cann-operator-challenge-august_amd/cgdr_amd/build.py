@@ -34,9 +34,10 @@ HIP_FLAGS = [
     "-Wno-inline-asm",
 ]
 
-SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip")]
+SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip"), os.path.join(CSRC, "cgdr_chunk_o.hip")]
 RUNNER_SOURCE = os.path.join(CSRC, "cgdr_golden_runner.cpp")
-HEADERS = [os.path.join(CSRC, "cgdr_kernels.h"), os.path.join(CSRC, "cgdr_schedule.h"), os.path.join(REPO_ROOT, "include", "cgdr_fwd_h.h")]
+HEADERS = [os.path.join(CSRC, n) for n in ("cgdr_kernels.h", "cgdr_schedule.h", "cgdr_host.h", "cgdr_chunk_o_kernel.h")] + \
+    [os.path.join(REPO_ROOT, "include", n) for n in ("cgdr_fwd_h.h", "cgdr_chunk_o.h")]
 
 
 def build_library(verbose: bool = False) -> str:

@@ -13,30 +13,18 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "cgdr_host.h"
 #include "cgdr_kernels.h"
 
 namespace {
 
-thread_local char g_last_error[512] = "";
-
-cgdr_status fail(cgdr_status st, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
-  va_end(ap);
-  return st;
-}
+using cgdr_host::env_int;
+using cgdr_host::fail;
 
 constexpr int64_t kMaxHeadDim = 256;     // docs/problem.txt:466 (Triton wrapper assert K <= 256)
 constexpr int64_t kMaxValueDim = 1024;   // V-tiling lifts the reference's K == V <= 256
 constexpr int64_t kMaxTasks = 1 << 30;
 constexpr int64_t kCUs = 256;            // MI355X compute units (one workgroup per CU)
-
-int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  if (s == nullptr || *s == 0) return dflt;
-  return atoi(s);
-}
 
 struct Plan {
   int kernel;        // 0 bf16 pipeline, 1 fp32
@@ -382,7 +370,7 @@ extern "C" {
 
 int cgdr_abi_version(void) { return CGDR_ABI_VERSION; }
 
-const char* cgdr_last_error(void) { return g_last_error; }
+const char* cgdr_last_error(void) { return cgdr_host::last_error; }
 
 const char* cgdr_status_string(cgdr_status status) {
   switch (status) {

@@ -871,7 +871,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 // g row of one chunk of one head is 256 contiguous bytes (4 cache lines) instead of 64 rows of
 // a token-major array (64 cache lines per chunk and workgroup).  One 64-token x 64-head tile
 // per workgroup, transposed through LDS: reads coalesced along heads, writes along tokens.
-__global__ void __launch_bounds__(256)
+// (static: each translation unit that includes this header gets its own copy)
+static __global__ void __launch_bounds__(256)
 cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, int64_t T, int64_t H,
                          int64_t sg_b, int64_t sg_t, int64_t sg_h) {
   __shared__ float tile[64][65];
@@ -889,7 +890,7 @@ cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, in
 
 // Zero n int32 counters (the helpers' progress counters) ahead of the chunk kernel; a kernel
 // rather than a memset so that the whole call can be captured in a HIP graph.
-__global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __restrict__ x, int64_t n) {
+static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __restrict__ x, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0;
 }
 

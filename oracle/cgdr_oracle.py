@@ -29,11 +29,20 @@ What it restates (paths relative to the reference's
 * ``safe_exp`` -- ``docs/problem.txt:272-274``.
 * ``wy_prepare`` -- the producer of (w, u, g) from (k, v, beta, per-token
   log-decay): ``chunk_gated_delta_rule_golden.py:102-124``.
+* ``chunk_o(..., rounding=None)`` -- the chunk output, the consumer of ``h`` and
+  ``v_new``: ``o_i = scale (e^{g_i} q_i h_c + sum_{j<=i in chunk} (q_i.k_j) e^{g_i-g_j} v_new_j)``,
+  the loop body of ``chunk_gated_delta_rule_golden.py:136-142`` (query pre-scaled at
+  ``:99-100``, decay mask ``:116``) and, on the device side, ``attn_inter`` of
+  ``ref/chunk_gated_delta_rule/op_kernel/arch22/chunk_gated_delta_rule_stage2.h:170`` plus
+  the masked ``q k^T`` product of ``.../chunk_gated_delta_rule_stage3.h:131-180``.
+  ``rounding="bf16"`` is the rounding model of the HIP kernel: the masked, decayed and
+  scaled ``q k^T`` is rounded to bf16 (it is an MFMA operand, as in stage3 ``:157-160``), both
+  products accumulate in fp32 and ``o`` is rounded once.
 * ``gated_delta_rule_tokenwise`` -- the token-by-token Gated DeltaNet recurrence
-  ``S_t = e^{a_t} (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T``.  It is
-  not in the reference; it is the textbook definition that the chunked form
-  must reproduce, and the tests use it to pin ``fwd_h`` independently of any
-  chunked restatement.
+  ``S_t = e^{a_t} (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T`` and, given
+  queries, its output ``o_t = scale S_t^T q_t``.  It is not in the reference; it is
+  the textbook definition that the chunked form must reproduce, and the tests use it
+  to pin ``fwd_h`` and ``chunk_o`` independently of any chunked restatement.
 
 Layouts are token-major (FLA / Triton wrapper ``docs/problem.txt:434-472``):
 k ``[B,T,Hg,K]``, w ``[B,T,H,K]``, u ``[B,T,H,V]``, g ``[B,T,H]``,
@@ -273,12 +282,15 @@ def wy_prepare(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
 def gated_delta_rule_tokenwise(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
                                initial_state: np.ndarray | None = None,
                                chunk_size: int = CHUNK_SIZE,
-                               cu_seqlens: np.ndarray | None = None):
+                               cu_seqlens: np.ndarray | None = None,
+                               q: np.ndarray | None = None, scale: float | None = None):
     """Token-by-token Gated DeltaNet state recurrence in float64.
 
     ``S_t = e^{a_t} (I - beta_t k_t k_t^T) S_{t-1} + beta_t k_t v_t^T`` with
     ``S`` of shape ``[K, V]``.  Returns the states entering every chunk,
-    ``[B, NT, H, K, V]``, and the final states ``[N, H, K, V]``.
+    ``[B, NT, H, K, V]``, and the final states ``[N, H, K, V]``; with queries ``q``
+    (``[B,T,H,K]``) also the outputs ``o_t = scale S_t^T q_t`` (``[B,T,H,V]``,
+    scale defaulting to ``K**-0.5``).
     """
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
@@ -287,6 +299,8 @@ def gated_delta_rule_tokenwise(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a
     seqs, NT = sequence_bounds(B, T, cu_seqlens, chunk_size)
     states = np.zeros((B, NT, H, K, V))
     final = np.zeros((len(seqs), H, K, V))
+    out = None if q is None else np.zeros((B, T, H, V))
+    sc = K ** -0.5 if scale is None else scale
     for n, (b, bos, eos, boh, _) in enumerate(seqs):
         for hh in range(H):
             S = np.zeros((K, V)) if initial_state is None else np.array(initial_state[n, hh], np.float64)
@@ -296,8 +310,88 @@ def gated_delta_rule_tokenwise(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a
                 kt, vt = k[b, t, hh], v[b, t, hh]
                 S = np.exp(a[b, t, hh]) * S
                 S = S + beta[b, t, hh] * np.outer(kt, vt - S.T @ kt)
+                if out is not None:
+                    out[b, t, hh] = sc * (S.T @ np.asarray(q[b, t, hh], np.float64))
             final[n, hh] = S
+    if out is not None:
+        return states, final, out
     return states, final
+
+
+# ----------------------------------------------------------------------------- chunk output
+
+def chunk_o(
+    q: np.ndarray,
+    k: np.ndarray,
+    v_new: np.ndarray,
+    h: np.ndarray,
+    g: np.ndarray | None = None,
+    scale: float | None = None,
+    chunk_size: int = CHUNK_SIZE,
+    cu_seqlens: np.ndarray | None = None,
+    rounding: str | None = None,
+    compute_dtype=np.float32,
+):
+    """Chunk output from the FwdH outputs, token-major layouts.
+
+    q, k ``[B,T,Hg,K]``, v_new ``[B,T,H,V]``, h ``[B,NT,H,K,V]`` (state entering each
+    chunk), g ``[B,T,H]`` (chunk-local cumulative log-decay, the FwdH gate) ->
+    o ``[B,T,H,V]``::
+
+        o_i = scale * ( e^{g_i} q_i . h_c  +  sum_{j <= i, j in chunk c} (q_i . k_j) e^{g_i - g_j} v_new_j )
+
+    (``chunk_gated_delta_rule_golden.py:136-142``: ``attn_inter + attn @ v_new`` with the
+    query scaled by ``scale`` (``:99-100``) and the decay mask ``exp((g_i - g_j).tril())``
+    kept on and below the diagonal (``:116``, ``:131-138``)).  ``scale`` defaults to
+    ``K**-0.5`` (``:99``).  ``rounding="bf16"``: the masked product
+    ``bf16(scale (q_i.k_j) e^{g_i-g_j})`` feeds the second product, both accumulate in
+    ``compute_dtype`` and ``o`` is rounded to bf16.
+    """
+    if chunk_size != CHUNK_SIZE:
+        raise ValueError(f"chunk_size must be {CHUNK_SIZE}, got {chunk_size}")
+    if rounding not in (None, "bf16"):
+        raise ValueError(f"unknown rounding {rounding!r}")
+    cd = np.dtype(compute_dtype)
+    q = np.asarray(q, cd)
+    k = np.asarray(k, cd)
+    v_new = np.asarray(v_new, cd)
+    h = np.asarray(h, cd)
+    B, T, Hg, K = q.shape
+    H, V = v_new.shape[2], v_new.shape[3]
+    if k.shape != q.shape or v_new.shape[:2] != (B, T) or H % Hg != 0:
+        raise ValueError("q and k must be [B,T,Hg,K], v_new [B,T,H,V] with H a multiple of Hg")
+    if cu_seqlens is not None and B != 1:
+        raise ValueError("cu_seqlens requires B == 1")
+    sc = cd.type(K ** -0.5 if scale is None else scale)
+    gq = None if g is None else np.asarray(g, cd)
+    head_of_key = np.arange(H) // (H // Hg)
+    seqs, NT = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    if h.shape != (B, NT, H, K, V):
+        raise ValueError(f"h must be {(B, NT, H, K, V)}")
+    o = np.zeros((B, T, H, V), dtype=cd)
+    for (b, bos, eos, boh, _) in seqs:
+        for c, t0 in enumerate(range(bos, eos, chunk_size)):
+            t1 = min(t0 + chunk_size, eos)
+            L = t1 - t0
+            Qc = np.transpose(q[b, t0:t1][:, head_of_key, :], (1, 0, 2))   # [H, L, K]
+            Kc = np.transpose(k[b, t0:t1][:, head_of_key, :], (1, 0, 2))   # [H, L, K]
+            Vc = np.transpose(v_new[b, t0:t1], (1, 0, 2))                   # [H, L, V]
+            A = np.matmul(Qc, np.transpose(Kc, (0, 2, 1)))                  # [H, L, L]
+            inter = np.matmul(Qc, h[b, boh + c])                            # [H, L, V]
+            tri = np.tril(np.ones((L, L), dtype=bool))
+            if gq is not None:
+                gc = np.transpose(gq[b, t0:t1], (1, 0))                     # [H, L]
+                diff = np.where(tri, gc[:, :, None] - gc[:, None, :], 0)
+                A = A * np.exp(diff).astype(cd)
+                inter = inter * np.exp(gc).astype(cd)[:, :, None]
+            A = np.where(tri, A * sc, 0).astype(cd)
+            if rounding:
+                A = bf16_round(A)
+            oc = inter * sc + np.matmul(A, Vc)
+            if rounding:
+                oc = bf16_round(oc)
+            o[b, t0:t1] = np.transpose(oc, (1, 0, 2))
+    return o
 
 
 # ----------------------------------------------------------------------------- synthetic inputs

@@ -24,7 +24,8 @@ def lib():
 
 
 def test_exports_every_declared_symbol(lib):
-    text = open(HEADER).read()
+    inc = os.path.dirname(HEADER)
+    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
     declared = set(re.findall(r"\b(cgdr_[a-z0-9_]+)\s*\(", text))
     assert declared == set(_abi.EXPORTED_SYMBOLS)
     for name in declared:
@@ -38,9 +39,13 @@ def test_struct_layout_matches_c(tmp_path):
 #include <stdio.h>
 #include <stddef.h>
 #include "cgdr_fwd_h.h"
+#include "cgdr_chunk_o.h"
 #define F(s, f) printf(#s "." #f " %zu\n", offsetof(s, f))
 int main(void) {
-  printf("args %zu\nplan %zu\n", sizeof(cgdr_fwd_h_args), sizeof(cgdr_fwd_h_plan));
+  printf("args %zu\nplan %zu\nochunk %zu\n", sizeof(cgdr_fwd_h_args), sizeof(cgdr_fwd_h_plan),
+         sizeof(cgdr_chunk_o_args));
+  F(cgdr_chunk_o_args, o); F(cgdr_chunk_o_args, chunk_size); F(cgdr_chunk_o_args, scale);
+  F(cgdr_chunk_o_args, in_dtype); F(cgdr_chunk_o_args, stride_q); F(cgdr_chunk_o_args, stride_o);
   F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
   F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, reserved0); F(cgdr_fwd_h_args, stride_k);
   F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final);
@@ -54,10 +59,12 @@ int main(void) {
                                                               check=True).stdout.split("\n") if line)
     assert int(out["args"]) == ctypes.sizeof(_abi.FwdHArgs)
     assert int(out["plan"]) == ctypes.sizeof(_abi.FwdHPlan)
+    assert int(out["ochunk"]) == ctypes.sizeof(_abi.ChunkOArgs)
+    classes = {"cgdr_fwd_h_args": _abi.FwdHArgs, "cgdr_fwd_h_plan": _abi.FwdHPlan, "cgdr_chunk_o_args": _abi.ChunkOArgs}
     for key, val in out.items():
         if "." in key:
             s, f = key.split(".")
-            cls = _abi.FwdHArgs if s == "cgdr_fwd_h_args" else _abi.FwdHPlan
+            cls = classes[s]
             assert getattr(cls, f).offset == int(val), key
 
 
