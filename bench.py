@@ -1,6 +1,6 @@
 """Benchmark of the ChunkGatedDeltaRuleFwdH hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--op fwd_h|chunk_o]
 
 A step is one FwdH call over the long-context prefill workload
 B=1, T=32768, H=Hg=32, K=V=128, bf16 k/w/u, fp32 g, h0=None, final state on
@@ -9,6 +9,11 @@ distributions of the CPU-runnable reference case) and resident in HBM before tim
 Prints one JSON line: whole-job tokens/s, the dominant kernel's achieved HBM bandwidth
 against MI355X's 8 TB/s, and the CPU oracle (numpy restatement of the reference chunk loop)
 timed on this host's cores on a bounded sample of the same workload.
+
+``--op chunk_o`` measures the chunk output (the consumer of FwdH's h and v_new) on the same
+workload shape instead: q, k [1,32768,32,128], v_new [1,32768,32,128], h [1,512,32,128,128]
+bf16 and fp32 g in HBM, one cgdr_chunk_o launch per step, with its own roofline and the numpy
+oracle's chunk_o as the CPU baseline.
 """
 
 from __future__ import annotations
@@ -71,10 +76,11 @@ def cpu_baseline(torch, k, w, u, g, sample_heads: int, repeats: int = 3):
     times = []
     with threadpool_limits(cores):
         O.fwd_h(kh[:, :2048], wh[:, :2048], uh[:, :2048], gh[:, :2048])      # warm-up
-        for _ in range(repeats):
+        for i in range(repeats):
             t0 = time.perf_counter()
             O.fwd_h(kh, wh, uh, gh)
             times.append(time.perf_counter() - t0)
+            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
     t = statistics.median(times)
     tokens = k.shape[0] * k.shape[1]
     frac = sample_heads / w.shape[2]
@@ -84,14 +90,136 @@ def cpu_baseline(torch, k, w, u, g, sample_heads: int, repeats: int = 3):
                        f"({t:.2f} s per run)")
 
 
+def chunk_o_bytes(B, T, H, Hg, K, V, NT, s=2):
+    """q, k, v_new, h and g read once, o written once."""
+    return B * T * Hg * K * s * 2 + B * T * H * V * s * 2 + B * NT * H * K * V * s + 4 * B * T * H
+
+
+def chunk_o_flops(B, NT, H, K, V):
+    """q k^T [64x64xK], q h [64xVxK], A' v [64xVx64] per chunk and head."""
+    return B * NT * H * 2 * 64 * (64 * K + K * V + 64 * V)
+
+
+def make_chunk_o_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    NT = (T + 63) // 64
+    q = torch.nn.functional.normalize(torch.randn(B, T, Hg, K, device=dev, generator=gen), dim=-1).to(torch.bfloat16)
+    k = torch.nn.functional.normalize(torch.randn(B, T, Hg, K, device=dev, generator=gen), dim=-1).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, device=dev, generator=gen).to(torch.bfloat16)
+    h = (torch.randn(B, NT, H, K, V, device=dev, generator=gen) * 0.3).to(torch.bfloat16)
+    inc = torch.nn.functional.logsigmoid(torch.randn(B, NT * 64, H, device=dev, generator=gen) + 3.0)
+    g = inc.view(B, NT, 64, H).cumsum(dim=2).view(B, NT * 64, H)[:, :T].contiguous()
+    return q, k, v, h, g
+
+
+def chunk_o_cpu_baseline(torch, q, k, v, h, g, sample_heads: int, repeats: int = 3):
+    from threadpoolctl import threadpool_limits
+
+    from oracle import cgdr_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    hs = slice(0, sample_heads)
+    arr = lambda t: t.float().cpu().numpy()
+    qh, kh, vh, hh, gh = arr(q[:, :, hs]), arr(k[:, :, hs]), arr(v[:, :, hs]), arr(h[:, :, hs]), arr(g[:, :, hs])
+    times = []
+    with threadpool_limits(cores):
+        O.chunk_o(qh[:, :2048], kh[:, :2048], vh[:, :2048], hh[:, :32], g=gh[:, :2048])   # warm-up
+        for i in range(repeats):
+            t0 = time.perf_counter()
+            O.chunk_o(qh, kh, vh, hh, g=gh)
+            times.append(time.perf_counter() - t0)
+            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
+    t = statistics.median(times)
+    frac = sample_heads / v.shape[2]
+    return dict(value=q.shape[0] * q.shape[1] * frac / t, unit="tokens/s", cores=cores, kind="port",
+                sample=f"numpy oracle chunk_o (exact fp32), B=1 T={q.shape[1]} on {sample_heads} of "
+                       f"{v.shape[2]} heads, median of {repeats}; value scaled to all heads ({t:.2f} s per run)")
+
+
+def progress(msg: str) -> None:
+    """One line per finished phase on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_steps(torch, dev, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def main_chunk_o(args, torch, cgdr_amd, dev):
+    W = WORKLOAD
+    B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
+    NT = (T + 63) // 64
+    q, k, v, h, g = make_chunk_o_inputs(torch, dev, B, T, H, Hg, K, V)
+    torch.cuda.synchronize()
+    progress("chunk_o inputs resident in HBM")
+    wall, kern_ms = time_steps(torch, dev, lambda: cgdr_amd.chunk_fwd_o(q, k, v, h, g=g), args.steps, args.warmup)
+    progress(f"timed {args.steps} chunk_o steps")
+    avg_ms = sum(kern_ms) / len(kern_ms)
+    nbytes = chunk_o_bytes(B, T, H, Hg, K, V, NT)
+    flops = chunk_o_flops(B, NT, H, K, V)
+    achieved = nbytes / (avg_ms * 1e-3) / 1e9
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "cgdr_chunk_o_bf16_T32768_H32_hbm_traffic.md")
+    if os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
+    out = {
+        "metric": "chunk output tokens/sec + achieved HBM GB/s at B=1,T=32k,H=32,K=V=128 bf16 (1 GPU)",
+        "value": B * T * args.steps / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "chunk output o from FwdH's h and v_new, long-context prefill", **W,
+                   "parallelism": "none (1 GPU)"},
+        "hbm_gbps": achieved,
+        "kernel_ms": avg_ms,
+        "kernel_ms_min": min(kern_ms),
+        "tflops": flops / (avg_ms * 1e-3) / 1e12,
+        "plan": cgdr_amd.chunk_o.plan(q, v),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = chunk_o_cpu_baseline(torch, q, k, v, h, g, args.cpu_sample_heads or 8,
+                                                   args.cpu_repeats or 3)
+        out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-sample-heads", type=int, default=32)
-    ap.add_argument("--cpu-repeats", type=int, default=7)
+    ap.add_argument("--cpu-sample-heads", type=int, default=None,
+                    help="heads of the CPU-baseline sample (default 32 for fwd_h, 8 for chunk_o)")
+    ap.add_argument("--cpu-repeats", type=int, default=None, help="default 7 for fwd_h, 3 for chunk_o")
+    ap.add_argument("--op", choices=("fwd_h", "chunk_o"), default="fwd_h",
+                    help="fwd_h: the headline FwdH step (default); chunk_o: the chunk output")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 elementwise copy (the reference kernel of known "
                          "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -105,6 +233,7 @@ def main():
 
     import cgdr_amd
 
+    progress("torch and cgdr_amd imported")
     dev = torch.device("cuda:0")
     if args.calibrate_copy:
         src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -115,11 +244,14 @@ def main():
         print(json.dumps({"calibration": "torch.mul(src, 1.0, out=dst)", "read_bytes": src.numel() * 4,
                           "write_bytes": dst.numel() * 4, "launches": 3}), flush=True)
         return
+    if args.op == "chunk_o":
+        return main_chunk_o(args, torch, cgdr_amd, dev)
     W = WORKLOAD
     B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
     NT = (T + 63) // 64
     k, w, u, g = make_inputs(torch, dev, B, T, H, Hg, K, V)
     torch.cuda.synchronize()
+    progress("fwd_h inputs resident in HBM")
 
     def step():
         return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, output_final_state=True)
@@ -141,6 +273,7 @@ def main():
     wall = time.perf_counter() - t0
     kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     avg_ms = sum(kern_ms) / len(kern_ms)
+    progress(f"timed {args.steps} fwd_h steps")
 
     nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, B)
     flops = algorithmic_flops(B, NT, H, K, V)
@@ -182,7 +315,7 @@ def main():
                      "algorithmic_bytes": nbytes},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads, args.cpu_repeats)
+        out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads or 32, args.cpu_repeats or 7)
         out["cpu_baseline"]["speedup"] = tokens_per_s / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
 
