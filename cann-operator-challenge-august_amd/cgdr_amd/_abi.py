@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI declared in ``include/cgdr_fwd_h.h`` and ``include/cgdr_chunk_o.h``.
+"""ctypes binding of the C ABI declared in ``include/cgdr_fwd_h.h``, ``include/cgdr_chunk_o.h``
+and ``include/cgdr_wy.h``.
 
 The shared library ``libcgdr_fwd_h.so`` is built in-tree by ``cgdr_amd.build`` into
 ``<package root>/lib``.  Loading it does not touch the GPU; only ``cgdr_fwd_h_launch``
@@ -33,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "cgdr_abi_version",
     "cgdr_chunk_o_launch",
     "cgdr_chunk_o_get_plan",
+    "cgdr_wy_launch",
 )
 
 _PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -126,6 +128,40 @@ class ChunkOArgs(ctypes.Structure):
     ]
 
 
+class WyArgs(ctypes.Structure):
+    """Mirror of ``cgdr_wy_args``."""
+
+    _fields_ = [
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("beta", ctypes.c_void_p),
+        ("g", ctypes.c_void_p),
+        ("cu_seqlens", ctypes.c_void_p),
+        ("chunk_indices", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("u", ctypes.c_void_p),
+        ("g_cumsum", ctypes.c_void_p),
+        ("B", ctypes.c_int64),
+        ("T", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("Hg", ctypes.c_int64),
+        ("K", ctypes.c_int64),
+        ("V", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("NT", ctypes.c_int64),
+        ("chunk_size", ctypes.c_int64),
+        ("in_dtype", ctypes.c_int32),
+        ("beta_dtype", ctypes.c_int32),
+        ("stride_k", ctypes.c_int64 * 3),
+        ("stride_v", ctypes.c_int64 * 3),
+        ("stride_beta", ctypes.c_int64 * 3),
+        ("stride_g", ctypes.c_int64 * 3),
+        ("stride_w", ctypes.c_int64 * 3),
+        ("stride_u", ctypes.c_int64 * 3),
+        ("stride_g_cumsum", ctypes.c_int64 * 3),
+    ]
+
+
 class CgdrError(RuntimeError):
     """A non-zero ``cgdr_status`` from the library, with its message."""
 
@@ -168,6 +204,8 @@ def load(path: str | None = None):
     lib.cgdr_chunk_o_get_plan.argtypes = [ctypes.POINTER(ChunkOArgs), ctypes.POINTER(ctypes.c_int32),
                                           ctypes.POINTER(ctypes.c_int64)]
     lib.cgdr_chunk_o_get_plan.restype = ctypes.c_int
+    lib.cgdr_wy_launch.argtypes = [ctypes.POINTER(WyArgs), ctypes.c_void_p]
+    lib.cgdr_wy_launch.restype = ctypes.c_int
     lib.cgdr_abi_version.argtypes = []
     lib.cgdr_abi_version.restype = ctypes.c_int
     if lib.cgdr_abi_version() != ABI_VERSION:
@@ -211,6 +249,10 @@ def launch(args: FwdHArgs, stream: int, workspace: int = 0, workspace_bytes: int
 
 def chunk_o_launch(args: ChunkOArgs, stream: int) -> None:
     check(load().cgdr_chunk_o_launch(ctypes.byref(args), ctypes.c_void_p(stream)))
+
+
+def wy_launch(args: WyArgs, stream: int) -> None:
+    check(load().cgdr_wy_launch(ctypes.byref(args), ctypes.c_void_p(stream)))
 
 
 def chunk_o_plan(args: ChunkOArgs) -> tuple[int, int]:

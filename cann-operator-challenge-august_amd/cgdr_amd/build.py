@@ -34,27 +34,47 @@ HIP_FLAGS = [
     "-Wno-inline-asm",
 ]
 
-SOURCES = [os.path.join(CSRC, "cgdr_fwd_h.hip"), os.path.join(CSRC, "cgdr_chunk_o.hip")]
+SOURCES = [os.path.join(CSRC, n) for n in ("cgdr_fwd_h.hip", "cgdr_chunk_o.hip", "cgdr_wy.hip")]
 RUNNER_SOURCE = os.path.join(CSRC, "cgdr_golden_runner.cpp")
-HEADERS = [os.path.join(CSRC, n) for n in ("cgdr_kernels.h", "cgdr_schedule.h", "cgdr_host.h", "cgdr_chunk_o_kernel.h")] + \
-    [os.path.join(REPO_ROOT, "include", n) for n in ("cgdr_fwd_h.h", "cgdr_chunk_o.h")]
+HEADERS = [os.path.join(CSRC, n) for n in ("cgdr_kernels.h", "cgdr_schedule.h", "cgdr_host.h", "cgdr_chunk_common.h",
+                                             "cgdr_chunk_o_kernel.h", "cgdr_wy_kernel.h")] + \
+    [os.path.join(REPO_ROOT, "include", n) for n in ("cgdr_fwd_h.h", "cgdr_chunk_o.h", "cgdr_wy.h")]
 
 
 def build_library(verbose: bool = False) -> str:
-    """Compile the library (always, even if a built copy exists) and return its path."""
+    """Compile the library (always, even if a built copy exists) and return its path.
+
+    Each translation unit is compiled in its own hipcc process (in parallel), then linked."""
     os.makedirs(LIB_DIR, exist_ok=True)
+    objs = [os.path.join(LIB_DIR, os.path.basename(src) + ".o") for src in SOURCES]
+    noise = "is not a recognized feature for this target"
+    cflags = [f for f in HIP_FLAGS if f != "-shared"]
+    procs = []
+    for src, obj in zip(SOURCES, objs):
+        cmd = [HIPCC, *cflags, "-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+    errors = []
+    for pr in procs:
+        _, err = pr.communicate()
+        err = "\n".join(l for l in (err or "").splitlines() if noise not in l)
+        if pr.returncode != 0:
+            errors.append(err)
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    if errors:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
     tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, *SOURCES, "-o", tmp]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (res.stderr or "").splitlines() if noise not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    for obj in objs:
+        os.remove(obj)
     return LIB_PATH
 
 

@@ -26,7 +26,7 @@
 // per-wave LDS row.  Rows past the chunk end are zero-filled, never read.
 #pragma once
 
-#include "cgdr_kernels.h"
+#include "cgdr_chunk_common.h"
 
 namespace cgdr {
 
@@ -63,47 +63,6 @@ struct ChunkOLayout {
   static constexpr int DMA_V = 64 / RPD;
 };
 
-// (sequence-relative) token range of one global chunk; len = 0 when the chunk maps to no
-// tokens (malformed metadata never leads to an access outside [0, T)).
-struct ChunkRange {
-  int64_t start;
-  int len;
-};
-
-__device__ __forceinline__ ChunkRange chunk_range(const ChunkOParams& p, int64_t chunk) {
-  ChunkRange r{0, 0};
-  int64_t start, end;
-  if (p.cu_seqlens == nullptr) {
-    start = chunk * kChunk;
-    end = p.T;
-  } else {
-    int64_t n, cc;
-    if (p.chunk_indices != nullptr) {
-      n = p.chunk_indices[2 * chunk];
-      cc = p.chunk_indices[2 * chunk + 1];
-      if (n < 0 || n >= p.N || cc < 0) return r;
-    } else {
-      int64_t boh = 0;
-      for (n = 0; n < p.N; ++n) {
-        const int64_t l = p.cu_seqlens[n + 1] - p.cu_seqlens[n];
-        const int64_t nc = l > 0 ? (l + kChunk - 1) / kChunk : 0;
-        if (chunk < boh + nc) break;
-        boh += nc;
-      }
-      if (n == p.N) return r;
-      cc = chunk - boh;
-    }
-    start = p.cu_seqlens[n] + cc * kChunk;
-    end = p.cu_seqlens[n + 1];
-  }
-  if (start < 0 || start >= p.T) return r;
-  if (end > p.T) end = p.T;
-  const int64_t len = end - start;
-  r.start = start;
-  r.len = len <= 0 ? 0 : (len > kChunk ? kChunk : (int)len);
-  return r;
-}
-
 template <int KD, int VT>
 __global__ void __launch_bounds__(256) cgdr_chunk_o_bf16_kernel(const ChunkOParams p) {
   using L = ChunkOLayout<KD, VT>;
@@ -126,7 +85,7 @@ __global__ void __launch_bounds__(256) cgdr_chunk_o_bf16_kernel(const ChunkOPara
   unit /= p.H;
   const int64_t chunk = unit % p.NT;
   const int b = (int)(unit / p.NT);
-  const ChunkRange cr = chunk_range(p, chunk);
+  const ChunkRange cr = chunk_range(p.T, p.N, p.cu_seqlens, p.chunk_indices, chunk);
   const int len = __builtin_amdgcn_readfirstlane(cr.len);
   if (len == 0) return;   // uniform over the workgroup
   const int64_t start = cr.start;
@@ -222,17 +181,7 @@ __global__ void __launch_bounds__(256) cgdr_chunk_o_bf16_kernel(const ChunkOPara
   // ---- O^T = h^T q^T (two transposed reads per operand: lane (G, n) gets
   // T[32 s + 8 G + 4 half + (0..3)][column 32 p + 8 (n / 4) + 4 x + n % 4])
   auto tr_op = [&](int off, int rbase, int pp, int x) {
-    u32x4 op;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int row = rbase + 8 * G + 4 * half + e;
-      const int piece = (4 * pp + qd) ^ swz_k<PV>(row);
-      const lds_char* a = (const lds_char*)smem + off + (row * PV + piece) * 16 + 8 * x;
-      const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a));
-      op[2 * half] = w[0];
-      op[2 * half + 1] = w[1];
-    }
-    return op;
+    return tr_operand<PV>((const lds_char*)smem + off, rbase, pp, x, G, e, qd);
   };
   f32x4 acc[NP][2];
 #pragma unroll

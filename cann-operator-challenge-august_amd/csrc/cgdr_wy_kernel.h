@@ -1,0 +1,306 @@
+// cgdr_wy_kernel.h -- gfx950 device code of the WY producer of FwdH's w, u and g.
+//
+// One workgroup (4 waves) owns one unit (batch row, chunk, value head).  With L <= 64 tokens,
+// per-token log-decay a, beta and keys k (key head of the value head), values v:
+//
+//   g_i  = a_0 + ... + a_i                                   (chunk-local cumsum, sequential)
+//   A_ij = beta_i (k_i . k_j) e^{g_i - g_j}  for j < i, else 0
+//   T    = (I + A)^{-1}                                      (unit lower triangular, fp32)
+//   w    = bf16( bf16(T diag(beta e^g)) k ),  u = bf16( bf16(T diag(beta)) v )
+//
+// (ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_golden.py:102-124 of the
+// reference, and its device stage 1, op_kernel/arch22/chunk_gated_delta_rule_stage1.h.)
+//
+// Phases, separated by workgroup barriers:
+//   0  DMA of the k and v tiles into LDS; wave 0 forms g (each lane sums a_0..a_i in order,
+//      which is the sequential cumsum bit for bit), beta e^g and beta
+//   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, k rows straight from HBM/L2),
+//      A written to LDS in fp32
+//   2  T: wave 0 inverts the four 16x16 diagonal blocks by forward substitution (lane = block,
+//      column); then T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj block by block in three levels
+//      (block distance 1, 2, 3) with fp32 MFMA 16x16x4.  The contraction slot of lane group G at
+//      step kk is 4 G + kk, so a C-layout result is directly the B operand of the next product.
+//   3  w^T = k^T T'^T and u^T = v^T T''^T with bf16 MFMA: the A operands are transposed reads of
+//      the k / v tiles, the B operands rows of T scaled per column and rounded to bf16; each lane
+//      ends with 8 consecutive columns of one token, written with 16-byte stores.
+#pragma once
+
+#include "cgdr_chunk_common.h"
+
+namespace cgdr {
+
+struct WyParams {
+  const void* k;
+  const void* v;
+  const void* beta;
+  const float* g;
+  const int64_t* cu_seqlens;
+  const int64_t* chunk_indices;
+  void* w;
+  void* u;
+  float* gc;
+  int64_t T, NT;
+  int32_t H, Hg, N, beta_f32;
+  int64_t sk_b, sk_t, sk_h;
+  int64_t sv_b, sv_t, sv_h;
+  int64_t sb_b, sb_t, sb_h;
+  int64_t sg_b, sg_t, sg_h;
+  int64_t sw_b, sw_t, sw_h;
+  int64_t su_b, su_t, su_h;
+  int64_t sc_b, sc_t, sc_h;
+};
+
+template <int KD, int VD>
+struct WyLayout {
+  static constexpr int PK = KD / 8, PV = VD / 8;   // 16-byte pieces per k / v tile row
+  static constexpr int MS = 68;                    // fp32 row stride of A and T (conflict-free columns)
+  static constexpr int K_OFF = 0;                  // k tile [64][KD] bf16
+  static constexpr int V_OFF = 64 * KD * 2;        // v tile [64][VD] bf16
+  static constexpr int A_OFF = V_OFF + 64 * VD * 2;
+  static constexpr int T_OFF = A_OFF + 64 * MS * 4;
+  static constexpr int G_OFF = T_OFF + 64 * MS * 4;   // g [64], beta e^g [64], beta [64], a [64]
+  static constexpr int LDS_BYTES = G_OFF + 4 * 256;
+  static constexpr int RPDK = 64 / PK, RPDV = 64 / PV;
+  static constexpr int DMA_K = 64 / RPDK, DMA_V = 64 / RPDV;
+};
+
+template <int KD, int VD>
+__global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
+  using L = WyLayout<KD, VD>;
+  constexpr int KS = KD / 32;
+  constexpr int MS = L::MS;
+  __shared__ __attribute__((aligned(1024))) char smem[L::LDS_BYTES];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, G = lane >> 4;
+  const int e = n >> 2, qd = n & 3;
+
+  // unit -> (b, chunk, head); consecutive units (the heads of one key head) share an XCD
+  int64_t unit = xcd_remap(blockIdx.x, gridDim.x);
+  const int head = (int)(unit % p.H);
+  unit /= p.H;
+  const int64_t chunk = unit % p.NT;
+  const int b = (int)(unit / p.NT);
+  const ChunkRange cr = chunk_range(p.T, p.N, p.cu_seqlens, p.chunk_indices, chunk);
+  const int len = __builtin_amdgcn_readfirstlane(cr.len);
+  if (len == 0) return;   // uniform over the workgroup
+  const int64_t start = cr.start;
+  const int kh = head / (p.H / p.Hg);
+
+  const __bf16* kb = (const __bf16*)p.k + b * p.sk_b + start * p.sk_t + kh * p.sk_h;
+  const __bf16* vb = (const __bf16*)p.v + b * p.sv_b + start * p.sv_t + head * p.sv_h;
+  __bf16* wb = (__bf16*)p.w + b * p.sw_b + start * p.sw_t + head * p.sw_h;
+  __bf16* ub = (__bf16*)p.u + b * p.su_b + start * p.su_t + head * p.su_h;
+
+  // ---- phase 0: k and v tiles (rows past the chunk end zero-filled)
+  const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
+  {
+    const int64_t krow = p.sk_t * 2, vrow = p.sv_t * 2;
+#pragma unroll
+    for (int m = 0; m < L::DMA_K; ++m) {
+      if (m % 4 != wave) continue;
+      const int r = m * L::RPDK + lane / L::PK, c = lane % L::PK;
+      if (r < len)
+        dma_b128(kb, (uint32_t)(r * krow) + 16u * (uint32_t)(c ^ swz_k<L::PK>(r)), lds0 + L::K_OFF + 1024u * m);
+      else
+        *(u32x4*)(smem + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int m = 0; m < L::DMA_V; ++m) {
+      if ((L::DMA_K + m) % 4 != wave) continue;
+      const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
+      if (r < len)
+        dma_b128(vb, (uint32_t)(r * vrow) + 16u * (uint32_t)(c ^ swz_k<L::PV>(r)), lds0 + L::V_OFF + 1024u * m);
+      else
+        *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+    }
+  }
+  // k rows for S = k k^T: rows j = 16 t + n (t <= wave) and this wave's columns i = 16 wave + n
+  // (a separate copy, so that no register array is indexed by the wave number)
+  const u32x4 zero4 = {0, 0, 0, 0};
+  u32x4 kf[4][KS], kc[KS];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int j = 16 * t + n;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kf[t][ks] = (t <= wave && j < len) ? *(const u32x4*)(kb + j * p.sk_t + 32 * ks + 8 * G) : zero4;
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+    kc[ks] = 16 * wave + n < len ? *(const u32x4*)(kb + (16 * wave + n) * p.sk_t + 32 * ks + 8 * G) : zero4;
+  float* GA = (float*)(smem + L::G_OFF);
+  if (wave == 0) {
+    float bt = 0.f, at = 0.f;
+    if (lane < len) {
+      const int64_t ob = b * p.sb_b + (start + lane) * p.sb_t + head * p.sb_h;
+      bt = p.beta_f32 ? ((const float*)p.beta)[ob] : (float)((const __bf16*)p.beta)[ob];
+      if (p.g != nullptr) at = p.g[b * p.sg_b + (start + lane) * p.sg_t + head * p.sg_h];
+    }
+    GA[192 + lane] = at;
+    wait_lgkm0();
+    // g_lane = ((a_0 + a_1) + a_2) + ... + a_lane, the order of a sequential cumsum
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 64; j += 4) {
+      const f32x4 a4 = *(const f32x4*)(GA + 192 + j);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (j + r <= lane) s += a4[r];
+    }
+    GA[lane] = s;
+    GA[64 + lane] = bt * expf(s);
+    GA[128 + lane] = bt;
+    if (p.gc != nullptr && lane < len) p.gc[b * p.sc_b + (start + lane) * p.sc_t + head * p.sc_h] = s;
+  }
+  wait_vm<0>();
+  wait_lgkm0();
+  block_barrier();
+
+  // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i); lane holds S[16t + 4G + r][i]
+  float* Am = (float*)(smem + L::A_OFF);
+  float* Tm = (float*)(smem + L::T_OFF);
+  const int i = 16 * wave + n;
+  {
+    const float gi = GA[i], bi = GA[128 + i];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (t > wave) continue;
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        c = mfma_bf16(__builtin_bit_cast(bf16x8, kf[t][ks]), __builtin_bit_cast(bf16x8, kc[ks]), c);
+      const f32x4 gj = *(const f32x4*)(GA + 16 * t + 4 * G);
+      f32x4 a;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * t + 4 * G + r;
+        a[r] = j < i ? bi * c[r] * expf(gi - gj[r]) : 0.f;
+      }
+      *(f32x4*)(Am + i * MS + 16 * t + 4 * G) = a;
+    }
+  }
+  wait_lgkm0();
+  block_barrier();
+
+  // ---- phase 2a: diagonal blocks T_bb = (I + A_bb)^{-1}, lane = (block bb, column c)
+  if (wave == 0) {
+    const int bb = lane >> 4, c = lane & 15;
+    float tcol[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float* arow = Am + (16 * bb + r) * MS + 16 * bb;
+      float acc = r == c ? 1.f : 0.f;
+#pragma unroll
+      for (int j = 0; j < r; ++j) acc -= arow[j] * tcol[j];
+      tcol[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) Tm[(16 * bb + r) * MS + 16 * bb + c] = tcol[r];
+  }
+  wait_lgkm0();
+  block_barrier();
+
+  // ---- phase 2b: off-diagonal blocks, one level per block distance
+  // acc += X[xr.., xc..] Y[yr.., yc..] (16x16 blocks of LDS matrices)
+  auto mm = [&](f32x4 acc, const float* X, int xr, int xc, const float* Y, int yr, int yc) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      acc = mfma_f32(X[(xr + n) * MS + xc + 4 * G + kk], Y[(yr + 4 * G + kk) * MS + yc + n], acc);
+    return acc;
+  };
+  // -(X[xr.., xc..] Y) stored into T[tr.., tc..], Y held in C layout
+  auto finish = [&](const f32x4& Y, int tr, int tc) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) acc = mfma_f32(Tm[(tr + n) * MS + tr + 4 * G + kk], Y[kk], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Tm[(tr + 4 * G + r) * MS + tc + n] = -acc[r];
+  };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  if (wave >= 1) {   // distance 1: T_{w,w-1} = -T_ww A_{w,w-1} T_{w-1,w-1}
+    const int bi = 16 * wave, bj = 16 * (wave - 1);
+    finish(mm(z4, Am, bi, bj, Tm, bj, bj), bi, bj);
+  }
+  wait_lgkm0();
+  block_barrier();
+  if (wave >= 2) {   // distance 2: T_{w,w-2} = -T_ww (A_{w,w-2} T_{w-2,w-2} + A_{w,w-1} T_{w-1,w-2})
+    const int bi = 16 * wave, bj = 16 * (wave - 2), bk = 16 * (wave - 1);
+    finish(mm(mm(z4, Am, bi, bj, Tm, bj, bj), Am, bi, bk, Tm, bk, bj), bi, bj);
+  }
+  wait_lgkm0();
+  block_barrier();
+  if (wave == 3) {   // distance 3: T_30 = -T_33 (A_30 T_00 + A_31 T_10 + A_32 T_20)
+    f32x4 x = mm(z4, Am, 48, 0, Tm, 0, 0);
+    x = mm(x, Am, 48, 16, Tm, 16, 0);
+    x = mm(x, Am, 48, 32, Tm, 32, 0);
+    finish(x, 48, 0);
+  }
+  wait_lgkm0();
+  block_barrier();
+  if (16 * wave >= len) return;
+
+  // ---- phase 3: w^T = k^T T'^T, u^T = v^T T''^T for this wave's tokens i
+  const int njp = (wave >> 1) + 1;   // contraction j <= i < 16 wave + 16
+  u32x4 bw[2], bu[2];
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp) {
+    if (jp >= njp) continue;
+    const int j0 = 32 * jp + 8 * G;
+    float tw[8], tu[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 t4 = *(const f32x4*)(Tm + i * MS + j0 + 4 * h);
+      const f32x4 sg = *(const f32x4*)(GA + 64 + j0 + 4 * h);
+      const f32x4 sb = *(const f32x4*)(GA + 128 + j0 + 4 * h);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool in = j0 + 4 * h + r <= i;
+        tw[4 * h + r] = in ? t4[r] * sg[r] : 0.f;
+        tu[4 * h + r] = in ? t4[r] * sb[r] : 0.f;
+      }
+    }
+    bw[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
+    bu[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
+  }
+  const lds_char* ktile = (const lds_char*)smem + L::K_OFF;
+  const lds_char* vtile = (const lds_char*)smem + L::V_OFF;
+  const bool store = i < len;
+#pragma unroll
+  for (int pp = 0; pp < KD / 32; ++pp) {
+    f32x4 acc[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+        if (jp < njp)
+          acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PK>(ktile, 32 * jp, pp, x, G, e, qd)),
+                             __builtin_bit_cast(bf16x8, bw[jp]), acc[x]);
+    }
+    if (store)
+      *(u32x4*)(wb + i * p.sw_t + 32 * pp + 8 * G) =
+          u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+  }
+#pragma unroll
+  for (int pp = 0; pp < VD / 32; ++pp) {
+    f32x4 acc[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int jp = 0; jp < 2; ++jp)
+        if (jp < njp)
+          acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PV>(vtile, 32 * jp, pp, x, G, e, qd)),
+                             __builtin_bit_cast(bf16x8, bu[jp]), acc[x]);
+    }
+    if (store)
+      *(u32x4*)(ub + i * p.su_t + 32 * pp + 8 * G) =
+          u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+  }
+}
+
+}  // namespace cgdr

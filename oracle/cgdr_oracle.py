@@ -244,7 +244,8 @@ def fwd_h(
 # ----------------------------------------------------------------------------- producer / textbook recurrence
 
 def wy_prepare(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
-               chunk_size: int = CHUNK_SIZE, cu_seqlens: np.ndarray | None = None):
+               chunk_size: int = CHUNK_SIZE, cu_seqlens: np.ndarray | None = None,
+               rounding: str | None = None):
     """(w, u, g) from keys, values, beta and per-token log-decay ``a`` (token-major).
 
     Restates ``chunk_gated_delta_rule_golden.py:102-124`` in float64: per chunk
@@ -252,13 +253,21 @@ def wy_prepare(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
     ``T = (I + A)^{-1}``, ``w = T (beta * e^g * k)``, ``u = T (beta * v)``.
     The reference's forward-substitution loop (``:117-121``) is replaced by a
     triangular solve, which is the same matrix.
-    k ``[B,T,H,K]`` (one key per value head), v ``[B,T,H,V]``, beta/a ``[B,T,H]``.
+    k ``[B,T,Hg,K]`` (head h uses key head h // (H/Hg)), v ``[B,T,H,V]``, beta/a ``[B,T,H]``.
+
+    ``rounding="bf16"`` is the rounding model of the HIP kernel: ``g`` is the float32
+    sequential cumsum, ``T`` stays exact, its columns are scaled by ``beta_j e^{g_j}`` (w) or
+    ``beta_j`` (u) and rounded to bf16 (the MFMA operand; the reference's bf16 variant rounds
+    ``T``, ``beta v`` and ``beta e^g k`` separately, ``chunk_gated_delta_rule_benchmark.py:79-88``),
+    the products accumulate exactly and w, u are rounded to bf16.
     """
+    if rounding not in (None, "bf16"):
+        raise ValueError(f"unknown rounding {rounding!r}")
     k = np.asarray(k, np.float64)
     v = np.asarray(v, np.float64)
     beta = np.asarray(beta, np.float64)
-    a = np.asarray(a, np.float64)
-    B, T, H, K = k.shape
+    B, T, Hg, K = k.shape
+    H = v.shape[2]
     w = np.zeros((B, T, H, K))
     u = np.zeros(v.shape)
     g = np.zeros((B, T, H))
@@ -267,14 +276,21 @@ def wy_prepare(k: np.ndarray, v: np.ndarray, beta: np.ndarray, a: np.ndarray,
         for t0 in range(bos, eos, chunk_size):
             t1 = min(t0 + chunk_size, eos)
             for hh in range(H):
-                kc, vc, bc = k[b, t0:t1, hh], v[b, t0:t1, hh], beta[b, t0:t1, hh]
-                gc = np.cumsum(a[b, t0:t1, hh])
+                kc, vc, bc = k[b, t0:t1, hh * Hg // H], v[b, t0:t1, hh], beta[b, t0:t1, hh]
+                if rounding:
+                    gc = np.cumsum(np.asarray(a[b, t0:t1, hh], np.float32), dtype=np.float32).astype(np.float64)
+                else:
+                    gc = np.cumsum(np.asarray(a[b, t0:t1, hh], np.float64))
                 L = t1 - t0
                 decay = np.exp(gc[:, None] - gc[None, :])
                 A = np.tril((bc[:, None] * (kc @ kc.T)) * decay, -1)
                 Tm = np.linalg.solve(np.eye(L) + A, np.eye(L))
-                w[b, t0:t1, hh] = Tm @ (bc[:, None] * np.exp(gc)[:, None] * kc)
-                u[b, t0:t1, hh] = Tm @ (bc[:, None] * vc)
+                if rounding:
+                    w[b, t0:t1, hh] = bf16_round(bf16_round(Tm * (bc * np.exp(gc))[None, :]) @ kc)
+                    u[b, t0:t1, hh] = bf16_round(bf16_round(Tm * bc[None, :]) @ vc)
+                else:
+                    w[b, t0:t1, hh] = Tm @ (bc[:, None] * np.exp(gc)[:, None] * kc)
+                    u[b, t0:t1, hh] = Tm @ (bc[:, None] * vc)
                 g[b, t0:t1, hh] = gc
     return w, u, g
 

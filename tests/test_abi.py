@@ -40,10 +40,13 @@ def test_struct_layout_matches_c(tmp_path):
 #include <stddef.h>
 #include "cgdr_fwd_h.h"
 #include "cgdr_chunk_o.h"
+#include "cgdr_wy.h"
 #define F(s, f) printf(#s "." #f " %zu\n", offsetof(s, f))
 int main(void) {
-  printf("args %zu\nplan %zu\nochunk %zu\n", sizeof(cgdr_fwd_h_args), sizeof(cgdr_fwd_h_plan),
-         sizeof(cgdr_chunk_o_args));
+  printf("args %zu\nplan %zu\nochunk %zu\nwy %zu\n", sizeof(cgdr_fwd_h_args), sizeof(cgdr_fwd_h_plan),
+         sizeof(cgdr_chunk_o_args), sizeof(cgdr_wy_args));
+  F(cgdr_wy_args, g_cumsum); F(cgdr_wy_args, chunk_size); F(cgdr_wy_args, beta_dtype);
+  F(cgdr_wy_args, stride_k); F(cgdr_wy_args, stride_g_cumsum);
   F(cgdr_chunk_o_args, o); F(cgdr_chunk_o_args, chunk_size); F(cgdr_chunk_o_args, scale);
   F(cgdr_chunk_o_args, in_dtype); F(cgdr_chunk_o_args, stride_q); F(cgdr_chunk_o_args, stride_o);
   F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
@@ -60,7 +63,9 @@ int main(void) {
     assert int(out["args"]) == ctypes.sizeof(_abi.FwdHArgs)
     assert int(out["plan"]) == ctypes.sizeof(_abi.FwdHPlan)
     assert int(out["ochunk"]) == ctypes.sizeof(_abi.ChunkOArgs)
-    classes = {"cgdr_fwd_h_args": _abi.FwdHArgs, "cgdr_fwd_h_plan": _abi.FwdHPlan, "cgdr_chunk_o_args": _abi.ChunkOArgs}
+    assert int(out["wy"]) == ctypes.sizeof(_abi.WyArgs)
+    classes = {"cgdr_fwd_h_args": _abi.FwdHArgs, "cgdr_fwd_h_plan": _abi.FwdHPlan, "cgdr_chunk_o_args": _abi.ChunkOArgs,
+               "cgdr_wy_args": _abi.WyArgs}
     for key, val in out.items():
         if "." in key:
             s, f = key.split(".")
