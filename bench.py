@@ -1,6 +1,6 @@
 """Benchmark of the ChunkGatedDeltaRuleFwdH hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--op fwd_h|chunk_o]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--op fwd_h|chunk_o|wy|forward]
 
 A step is one FwdH call over the long-context prefill workload
 B=1, T=32768, H=Hg=32, K=V=128, bf16 k/w/u, fp32 g, h0=None, final state on
@@ -13,7 +13,9 @@ timed on this host's cores on a bounded sample of the same workload.
 ``--op chunk_o`` measures the chunk output (the consumer of FwdH's h and v_new) on the same
 workload shape instead: q, k [1,32768,32,128], v_new [1,32768,32,128], h [1,512,32,128,128]
 bf16 and fp32 g in HBM, one cgdr_chunk_o launch per step, with its own roofline and the numpy
-oracle's chunk_o as the CPU baseline.
+oracle's chunk_o as the CPU baseline.  ``--op wy`` measures the WY producer (k, v, beta, the
+per-token log-decay -> w, u, g) and ``--op forward`` the whole chunked forward (WY -> FwdH ->
+chunk output, q k v beta g -> o and the final state) on the same shape.
 """
 
 from __future__ import annotations
@@ -160,6 +162,100 @@ def time_steps(torch, dev, step, steps, warmup):
     return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
 
 
+def wy_bytes(B, T, H, Hg, K, V, s=2):
+    """k, v, beta (fp32), g read once; w, u, g_cumsum written once."""
+    return B * T * (Hg * K + H * V) * s + 8 * B * T * H + B * T * H * (K + V) * s + 4 * B * T * H
+
+
+def make_wy_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    k = torch.nn.functional.normalize(torch.randn(B, T, Hg, K, device=dev, generator=gen), dim=-1).to(torch.bfloat16)
+    v = torch.randn(B, T, H, V, device=dev, generator=gen).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, T, H, device=dev, generator=gen))
+    a = torch.nn.functional.logsigmoid(torch.randn(B, T, H, device=dev, generator=gen) + 2.0)
+    q = torch.nn.functional.normalize(torch.randn(B, T, Hg, K, device=dev, generator=gen), dim=-1).to(torch.bfloat16)
+    return q, k, v, beta, a
+
+
+def wy_cpu_baseline(torch, k, v, beta, a, sample_heads, repeats):
+    from threadpoolctl import threadpool_limits
+
+    from oracle import cgdr_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    hs = slice(0, sample_heads)
+    arr = lambda t: t.float().cpu().numpy()
+    kh, vh, bh, ah = arr(k[:, :, hs]), arr(v[:, :, hs]), arr(beta[:, :, hs]), arr(a[:, :, hs])
+    times = []
+    with threadpool_limits(cores):
+        O.wy_prepare(kh[:, :256], vh[:, :256], bh[:, :256], ah[:, :256])   # warm-up
+        for i in range(repeats):
+            t0 = time.perf_counter()
+            O.wy_prepare(kh, vh, bh, ah)
+            times.append(time.perf_counter() - t0)
+            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
+    t = statistics.median(times)
+    frac = sample_heads / v.shape[2]
+    return dict(value=k.shape[0] * k.shape[1] * frac / t, unit="tokens/s", cores=cores, kind="port",
+                sample=f"numpy oracle wy_prepare (float64, one solve per chunk and head), B=1 T={k.shape[1]} "
+                       f"on {sample_heads} of {v.shape[2]} heads, median of {repeats}; value scaled to all heads "
+                       f"({t:.2f} s per run)")
+
+
+def main_wy(args, torch, cgdr_amd, dev, forward: bool):
+    W = WORKLOAD
+    B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
+    NT = (T + 63) // 64
+    q, k, v, beta, a = make_wy_inputs(torch, dev, B, T, H, Hg, K, V)
+    torch.cuda.synchronize()
+    progress("wy inputs resident in HBM")
+    if forward:
+        step = lambda: cgdr_amd.chunk_gated_delta_rule_fwd(q, k, v, a, beta, output_final_state=True)
+        nbytes = (wy_bytes(B, T, H, Hg, K, V) + algorithmic_bytes(B, T, H, Hg, K, V, NT, B)
+                  + chunk_o_bytes(B, T, H, Hg, K, V, NT))
+        name, tfile = "forward", None
+    else:
+        step = lambda: cgdr_amd.wy_fwd(k, v, beta, g=a)
+        nbytes = wy_bytes(B, T, H, Hg, K, V)
+        name, tfile = "wy", os.path.join(ROOT, "profiles", "cgdr_wy_bf16_T32768_H32_hbm_traffic.md")
+    wall, kern_ms = time_steps(torch, dev, step, args.steps, args.warmup)
+    progress(f"timed {args.steps} {name} steps")
+    avg_ms = sum(kern_ms) / len(kern_ms)
+    achieved = nbytes / (avg_ms * 1e-3) / 1e9
+    traffic = None
+    if tfile and os.path.exists(tfile):
+        for line in open(tfile):
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = int(line.split(":")[1])
+    what = ("chunked forward o, final_state from q, k, v, beta, g (WY -> FwdH -> chunk output)" if forward
+            else "WY producer w, u, g_cumsum from k, v, beta, g")
+    out = {
+        "metric": f"{name} tokens/sec + achieved HBM GB/s at B=1,T=32k,H=32,K=V=128 bf16 (1 GPU)",
+        "value": B * T * args.steps / wall,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": what + ", long-context prefill", **W, "parallelism": "none (1 GPU)"},
+        "hbm_gbps": achieved,
+        "kernel_ms": avg_ms,
+        "kernel_ms_min": min(kern_ms),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline and not forward:
+        out["cpu_baseline"] = wy_cpu_baseline(torch, k, v, beta, a, args.cpu_sample_heads or 8, args.cpu_repeats or 3)
+        out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
+    print(json.dumps(out), flush=True)
+
+
 def main_chunk_o(args, torch, cgdr_amd, dev):
     W = WORKLOAD
     B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
@@ -218,8 +314,9 @@ def main():
     ap.add_argument("--cpu-sample-heads", type=int, default=None,
                     help="heads of the CPU-baseline sample (default 32 for fwd_h, 8 for chunk_o)")
     ap.add_argument("--cpu-repeats", type=int, default=None, help="default 7 for fwd_h, 3 for chunk_o")
-    ap.add_argument("--op", choices=("fwd_h", "chunk_o"), default="fwd_h",
-                    help="fwd_h: the headline FwdH step (default); chunk_o: the chunk output")
+    ap.add_argument("--op", choices=("fwd_h", "chunk_o", "wy", "forward"), default="fwd_h",
+                    help="fwd_h: the headline FwdH step (default); chunk_o: the chunk output; wy: the WY "
+                         "producer; forward: WY -> FwdH -> chunk output")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 elementwise copy (the reference kernel of known "
                          "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -246,6 +343,8 @@ def main():
         return
     if args.op == "chunk_o":
         return main_chunk_o(args, torch, cgdr_amd, dev)
+    if args.op in ("wy", "forward"):
+        return main_wy(args, torch, cgdr_amd, dev, forward=args.op == "forward")
     W = WORKLOAD
     B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
     NT = (T + 63) // 64
