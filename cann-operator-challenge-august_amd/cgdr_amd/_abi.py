@@ -23,6 +23,9 @@ CGDR_ERR_LAUNCH = 4
 CGDR_BF16 = 0
 CGDR_F32 = 1
 
+CGDR_NUMERICS_DEFAULT = 0
+CGDR_NUMERICS_CONTEST = 1
+
 EXPORTED_SYMBOLS = (
     "cgdr_fwd_h_workspace_size",
     "cgdr_fwd_h_launch",
@@ -70,7 +73,7 @@ class FwdHArgs(ctypes.Structure):
         ("in_dtype", ctypes.c_int32),
         ("h0_dtype", ctypes.c_int32),
         ("final_dtype", ctypes.c_int32),
-        ("reserved0", ctypes.c_int32),
+        ("numerics", ctypes.c_int32),
         ("stride_k", ctypes.c_int64 * 3),
         ("stride_w", ctypes.c_int64 * 3),
         ("stride_u", ctypes.c_int64 * 3),

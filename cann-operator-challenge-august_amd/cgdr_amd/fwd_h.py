@@ -27,6 +27,10 @@ from . import _abi
 CHUNK_SIZE = _abi.CHUNK_SIZE
 
 _DTYPES = {torch.bfloat16: _abi.CGDR_BF16, torch.float32: _abi.CGDR_F32}
+# "default": the Triton kernel's rounding model (docs/problem.txt:330-432) for bf16 inputs,
+# exact fp32 for fp32 inputs; "contest": the contest reference run()'s fp16-saturating,
+# bf16-state numerics (docs/problem.txt:81-167), bf16 inputs only.
+_NUMERICS = {"default": _abi.CGDR_NUMERICS_DEFAULT, "contest": _abi.CGDR_NUMERICS_CONTEST}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -78,7 +82,7 @@ def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets,
 
 
 def _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT,
-            strides: dict) -> None:
+            strides: dict, numerics: str = "default") -> None:
     a = _abi.FwdHArgs()
     a.k, a.w, a.u = k.data_ptr(), w.data_ptr(), u.data_ptr()
     a.g = _ptr(g)
@@ -91,6 +95,9 @@ def _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V
     a.in_dtype = _DTYPES[k.dtype]
     a.h0_dtype = _DTYPES[h0.dtype] if h0 is not None else _abi.CGDR_F32
     a.final_dtype = _DTYPES[final.dtype] if final is not None else _abi.CGDR_F32
+    if numerics not in _NUMERICS:
+        raise ValueError(f"numerics must be one of {sorted(_NUMERICS)}, got {numerics!r}")
+    a.numerics = _NUMERICS[numerics]
     for name in ("stride_k", "stride_w", "stride_u", "stride_g", "stride_h", "stride_v",
                  "stride_h0", "stride_final"):
         vals = strides.get(name)
@@ -135,8 +142,10 @@ def chunk_gated_delta_rule_fwd_h(
     chunk_indices: torch.Tensor | None = None,
     chunk_offsets: torch.Tensor | None = None,
     final_state_dtype: torch.dtype = torch.float32,
+    numerics: str = "default",
 ):
     """``(h, v_new, final_state)`` for token-major inputs; see the module docstring.
+    ``numerics="contest"`` selects the contest reference's rounding model (bf16 inputs).
 
     ``g`` and ``initial_state`` may be any floating dtype; g is used in fp32 and
     initial_state in fp32 or bf16 (other dtypes are upcast to fp32).
@@ -185,17 +194,18 @@ def chunk_gated_delta_rule_fwd_h(
         stride_h0=h0.stride()[:2] if h0 is not None else None,
         stride_final=final.stride()[:2] if final is not None else None,
     )
-    _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT, strides)
+    _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT, strides, numerics)
     return h, v_new, final
 
 
-def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_SIZE):
+def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_SIZE, numerics="default"):
     """Contest reference signature (``docs/problem.txt:81``), head-major layouts.
 
     k ``[B,T,HK,K]``, w ``[B,HV,T,K]``, u ``[B,HV,T,V]``, g ``[B,HV,T]``, initial_state
     ``[N,HV,K,V]`` (or None) -> ``(S [B,HV,NT,K,V], v [B,HV,T,V], final_state [N,HV,K,V])``.
-    The state recurrence keeps fp32 state (the Triton rounding model), so ``S`` is k's dtype
-    and ``final_state`` u's dtype as in the reference's output declaration.
+    By default the state recurrence keeps fp32 state (the Triton rounding model);
+    ``numerics="contest"`` reproduces run()'s own casts (bf16 state, saturating fp16).  ``S``
+    is k's dtype and ``final_state`` u's dtype as in the reference's output declaration.
     """
     _check_common(k, w, u, g, initial_state, chunk_size)
     B, T, Hg, K = k.shape
@@ -235,7 +245,7 @@ def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_S
         stride_h0=h0.stride()[:2] if h0 is not None else None,
         stride_final=final.stride()[:2],
     )
-    _launch(k, w, u, g, h0, cu_dev, offs_dev, S, v, final, B, T, H, Hg, K, V, N, NT, strides)
+    _launch(k, w, u, g, h0, cu_dev, offs_dev, S, v, final, B, T, H, Hg, K, V, N, NT, strides, numerics)
     return S, v, final
 
 

@@ -53,6 +53,10 @@ cgdr_status validate(const cgdr_fwd_h_args* a) {
     return fail(CGDR_ERR_INVALID, "h0_dtype %d is not a cgdr_dtype", a->h0_dtype);
   if (a->final_state != nullptr && a->final_dtype != CGDR_BF16 && a->final_dtype != CGDR_F32)
     return fail(CGDR_ERR_INVALID, "final_dtype %d is not a cgdr_dtype", a->final_dtype);
+  if (a->numerics != CGDR_NUMERICS_DEFAULT && a->numerics != CGDR_NUMERICS_CONTEST)
+    return fail(CGDR_ERR_INVALID, "numerics %d is not a cgdr_numerics", a->numerics);
+  if (a->numerics == CGDR_NUMERICS_CONTEST && a->in_dtype != CGDR_BF16)
+    return fail(CGDR_ERR_UNSUPPORTED, "contest numerics are defined for bf16 inputs only");
   if (a->B < 1) return fail(CGDR_ERR_INVALID, "B must be >= 1, but got %lld", (long long)a->B);
   if (a->T < 1) return fail(CGDR_ERR_INVALID, "T must be >= 1, but got %lld", (long long)a->T);
   if (a->H < 1 || a->Hg < 1)
@@ -166,7 +170,14 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
   }
   if (V % (16 * ncw) != 0) ncw = 1;
-  if (a->in_dtype == CGDR_F32) {
+  if (a->numerics == CGDR_NUMERICS_CONTEST) {
+    pl->kernel = 2;
+    pl->ncw = ncw;
+    pl->nlw = 0;
+    pl->stages = 1;
+    pl->threads = 64 * ncw;
+    pl->lds = 0;
+  } else if (a->in_dtype == CGDR_F32) {
     pl->kernel = 1;
     pl->ncw = ncw;
     pl->nlw = 0;
@@ -245,10 +256,11 @@ hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t str
   return hipGetLastError();
 }
 
-template <int KD, int NCW>
+template <int KD, int NCW, bool CONTEST>
 hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
   using L = cgdr::F32Layout<KD, NCW>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream, p);
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW, CONTEST>), dim3((unsigned)tasks), dim3(L::THREADS), 0,
+                     stream, p);
   return hipGetLastError();
 }
 
@@ -320,19 +332,25 @@ int bf16_max_stages(int64_t K, int ncw, int nlw) {
   }
 }
 
-template <int KD>
+template <int KD, bool CONTEST>
 hipError_t dispatch_f32(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
-  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
-  return launch_f32<KD, 1>(p, pl.tasks, s);
+  if (pl.ncw == 2) return launch_f32<KD, 2, CONTEST>(p, pl.tasks, s);
+  if (pl.ncw == 4) return launch_f32<KD, 4, CONTEST>(p, pl.tasks, s);
+  return launch_f32<KD, 1, CONTEST>(p, pl.tasks, s);
 }
 
 int lds_bytes_of(const Plan& pl, int64_t K) {
-  if (pl.kernel == 1) {
+  if (pl.kernel == 1 || pl.kernel == 2) {
+    auto f32 = [&](auto kd) -> int {
+      constexpr int KD = decltype(kd)::value;
+      return pl.ncw == 1 ? cgdr::F32Layout<KD, 1>::LDS_BYTES
+                         : pl.ncw == 2 ? cgdr::F32Layout<KD, 2>::LDS_BYTES : cgdr::F32Layout<KD, 4>::LDS_BYTES;
+    };
     switch (K) {
-      case 32: return pl.ncw == 1 ? cgdr::F32Layout<32, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<32, 2>::LDS_BYTES : cgdr::F32Layout<32, 4>::LDS_BYTES;
-      case 64: return pl.ncw == 1 ? cgdr::F32Layout<64, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<64, 2>::LDS_BYTES : cgdr::F32Layout<64, 4>::LDS_BYTES;
-      default: return pl.ncw == 1 ? cgdr::F32Layout<128, 1>::LDS_BYTES : pl.ncw == 2 ? cgdr::F32Layout<128, 2>::LDS_BYTES : cgdr::F32Layout<128, 4>::LDS_BYTES;
+      case 32: return f32(std::integral_constant<int, 32>{});
+      case 64: return f32(std::integral_constant<int, 64>{});
+      case 128: return f32(std::integral_constant<int, 128>{});
+      default: return f32(std::integral_constant<int, 256>{});
     }
   }
   // bf16: the layout of the instantiated kernel
@@ -444,11 +462,18 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
       case 128: e = dispatch_bf16<128>(p, pl, s); break;
       default: e = dispatch_bf16<256>(p, pl, s); break;
     }
+  } else if (pl.kernel == 1) {
+    switch (args->K) {
+      case 32: e = dispatch_f32<32, false>(p, pl, s); break;
+      case 64: e = dispatch_f32<64, false>(p, pl, s); break;
+      default: e = dispatch_f32<128, false>(p, pl, s); break;
+    }
   } else {
     switch (args->K) {
-      case 32: e = dispatch_f32<32>(p, pl, s); break;
-      case 64: e = dispatch_f32<64>(p, pl, s); break;
-      default: e = dispatch_f32<128>(p, pl, s); break;
+      case 32: e = dispatch_f32<32, true>(p, pl, s); break;
+      case 64: e = dispatch_f32<64, true>(p, pl, s); break;
+      case 128: e = dispatch_f32<128, true>(p, pl, s); break;
+      default: e = dispatch_f32<256, true>(p, pl, s); break;
     }
   }
   if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));

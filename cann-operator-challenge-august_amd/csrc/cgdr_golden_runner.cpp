@@ -22,10 +22,15 @@
 //     its largest golden magnitude, and v within rtol=2e-2, atol=2e-3 for all but 0.1% of
 //     elements (the golden state is rounded to bf16 after every chunk, this operator keeps it
 //     in fp32, so h and final differ by about one bf16 step of the state),
+//   * with --contest runs the contest reference's own numerics (CGDR_NUMERICS_CONTEST: bf16
+//     state, saturating fp16 casts), the numerics the golden files were generated with, and
+//     --check then also reports the fraction of elements meeting the contest tolerance
+//     (bit-equal, |err| <= 1e-6 or |err| <= 1e-5 |golden|, code/examples/compare_npu_output.py:14-15,54-73)
+//     and requires at least 98% of them,
 //   * with --repeat R times R further launches with HIP events,
 //   * with --dry-run stops after validation and planning, before any device call.
 //
-// Usage: cgdr_golden_runner CASE_DIR [--out DIR] [--device N] [--check] [--repeat R] [--dry-run]
+// Usage: cgdr_golden_runner CASE_DIR [--out DIR] [--device N] [--check] [--contest] [--repeat R] [--dry-run]
 // Exit status: 0 success, 1 comparison failure, 2 usage / input / runtime error.
 
 #include <hip/hip_runtime.h>
@@ -359,7 +364,7 @@ float bf16_to_float(uint16_t b) {
 // Comparison of one bf16 output with its golden counterpart.
 struct Compare {
   double max_err = 0, scale = 0;
-  int64_t outside = 0, n = 0;
+  int64_t outside = 0, n = 0, contest_ok = 0;
 };
 
 Compare compare_bf16(const std::vector<uint8_t>& got, const std::vector<uint8_t>& want) {
@@ -373,6 +378,7 @@ Compare compare_bf16(const std::vector<uint8_t>& got, const std::vector<uint8_t>
     c.max_err = std::max(c.max_err, e);
     c.scale = std::max(c.scale, std::fabs(y));
     if (!(e <= 2e-3 + 2e-2 * std::fabs(y))) ++c.outside;
+    if (a[i] == b[i] || e <= 1e-6 || e <= 1e-5 * std::fabs(y)) ++c.contest_ok;
   }
   c.n = static_cast<int64_t>(n);
   return c;
@@ -381,12 +387,13 @@ Compare compare_bf16(const std::vector<uint8_t>& got, const std::vector<uint8_t>
 struct Options {
   fs::path case_dir, out_dir;
   int device = 0;
-  bool check = false, dry_run = false;
+  bool check = false, dry_run = false, contest = false;
   int repeat = 0;
 };
 
 [[noreturn]] void usage() {
-  std::cerr << "usage: cgdr_golden_runner CASE_DIR [--out DIR] [--device N] [--check] [--repeat R] [--dry-run]\n";
+  std::cerr << "usage: cgdr_golden_runner CASE_DIR [--out DIR] [--device N] [--check] [--contest] [--repeat R] "
+               "[--dry-run]\n";
   std::exit(2);
 }
 
@@ -399,6 +406,7 @@ Options parse_args(int argc, char** argv) {
     else if (a == "--device") o.device = std::stoi(next());
     else if (a == "--repeat") o.repeat = std::stoi(next());
     else if (a == "--check") o.check = true;
+    else if (a == "--contest") o.contest = true;
     else if (a == "--dry-run") o.dry_run = true;
     else if (a == "-h" || a == "--help") usage();
     else if (!a.empty() && a[0] == '-') usage();
@@ -457,6 +465,7 @@ int run_case(const Options& opt) {
   std::memset(&a, 0, sizeof a);
   a.B = 1; a.T = T; a.H = HV; a.Hg = HK; a.K = D; a.V = D; a.N = N; a.NT = NT; a.chunk_size = 64;
   a.in_dtype = CGDR_BF16; a.h0_dtype = CGDR_BF16; a.final_dtype = CGDR_BF16;
+  a.numerics = opt.contest ? CGDR_NUMERICS_CONTEST : CGDR_NUMERICS_DEFAULT;
   const int64_t sk[3] = {T * HK * D, HK * D, D}, sw[3] = {HV * T * D, D, T * D};
   const int64_t sg[3] = {HV * T, 1, T}, sh[3] = {HV * NT * D * D, D * D, NT * D * D};
   const int64_t s0[2] = {HV * D * D, D * D};
@@ -563,11 +572,13 @@ int run_case(const Options& opt) {
     HostTensor gold = load_tensor(opt.case_dir, manifest, o.golden, true);
     if (gold.data.size() != o.got->size()) throw std::runtime_error(std::string(o.golden) + ": size mismatch");
     Compare c = compare_bf16(*o.got, gold.data);
+    const double contest_frac = c.n ? static_cast<double>(c.contest_ok) / c.n : 1.0;
     const bool pass = c.max_err <= 1e-2 * std::max(c.scale, 1e-30) &&
-                      (!o.elementwise || c.outside <= c.n / 1000);
-    std::printf("%s %-11s max_abs_err=%.3e scale=%.3e outside(rtol=2e-2,atol=2e-3)=%lld/%lld\n",
+                      (!o.elementwise || c.outside <= c.n / 1000) && (!opt.contest || contest_frac >= 0.98);
+    std::printf("%s %-11s max_abs_err=%.3e scale=%.3e outside(rtol=2e-2,atol=2e-3)=%lld/%lld "
+                "contest_tolerance=%.5f\n",
                 pass ? "PASS" : "FAIL", o.name, c.max_err, c.scale, static_cast<long long>(c.outside),
-                static_cast<long long>(c.n));
+                static_cast<long long>(c.n), contest_frac);
     ok = ok && pass;
   }
   std::cout << (ok ? "Case passed" : "Case FAILED") << std::endl;

@@ -899,7 +899,30 @@ static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __re
 // (pi, sigma) with v_mfma_f32_16x16x4_f32, whose operands are one element per lane, so no
 // transposed reads are needed.  All waves load the next chunk with plain loads; it is the
 // exact-arithmetic path (fp32 products, fp32 accumulation) and is not the performance path.
+//
+// CONTEST = true is the same kernel for bf16 k/w/u with the numerics of the contest reference
+// run() (docs/problem.txt:81-167; code/tests/golden/generate_golden.py:350-440), "O2":
+//   state S in bf16;  ws = bf16(W S);  v16 = f16sat(f16sat(u) - nan_to_num(fp16(ws)))
+//   v_new = bf16(v16);  vd = bf16(f16sat(v16 * f16sat(exp(g_last - g))))
+//   hd = f16sat(f16sat(S) * fp16(exp(fp16(g_last))));  up = nan_to_num(fp16(bf16(K^T vd)))
+//   S = bf16(bf16(hd) + bf16(up))
+// where f16sat is the reference's cast_to_float16 (round to fp16, finite overflow saturates to
+// +-65504, inf and NaN pass through).  bf16 values are exact in fp32, so the fp32 MFMA products
+// are the bf16 GEMM's products, accumulated in fp32 and rounded once to bf16.
 // =============================================================================================
+
+// cast_to_float16 (code/tests/golden/generate_golden.py:285-290), returned as its fp32 value
+__device__ __forceinline__ float f16_sat(float x) {
+  float r = (float)(_Float16)x;
+  if (__builtin_isfinite(x)) r = fminf(fmaxf(r, -65504.f), 65504.f);
+  return r;
+}
+// torch.nan_to_num(x.to(float16), nan=0, posinf=inf, neginf=-inf)
+__device__ __forceinline__ float f16_nan_to_num(float x) {
+  const float r = (float)(_Float16)x;
+  return r != r ? 0.f : r;
+}
+__device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
 template <int KD, int NCW>
 struct F32Layout {
   static constexpr int VT = 16 * NCW;
@@ -912,7 +935,7 @@ struct F32Layout {
   static constexpr int THREADS = 64 * NCW;
 };
 
-template <int KD, int NCW>
+template <int KD, int NCW, bool CONTEST = false>
 __global__ void __launch_bounds__(64 * NCW)
 cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   using L = F32Layout<KD, NCW>;
@@ -933,12 +956,14 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   const int g = lane >> 4, n = lane & 15;
   const int vcol = vbase + 16 * wave + n;
 
-  const float* kb_ = (const float*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
-  const float* wb_ = (const float*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
-  const float* ub_ = (const float*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
+  // element type of k/w/u/h/v_new: fp32, or bf16 in contest mode
+  using E = std::conditional_t<CONTEST, __bf16, float>;
+  const E* kb_ = (const E*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
+  const E* wb_ = (const E*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
+  const E* ub_ = (const E*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
   const float* gb_ = p.g == nullptr ? nullptr : p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h;
-  float* hb_ = (float*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h;
-  float* vb_ = p.v_new == nullptr ? nullptr : (float*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h;
+  E* hb_ = (E*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h;
+  E* vb_ = p.v_new == nullptr ? nullptr : (E*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h;
 
   f32x4 S[KT];
   if (p.h0 != nullptr) {
@@ -950,6 +975,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (int64_t)krow * p.V + vcol;
         S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
+        if constexpr (CONTEST) S[kt][r] = bf16_rnd(S[kt][r]);   // the state is bf16
       }
   } else {
 #pragma unroll
@@ -962,12 +988,12 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     __syncthreads();
     for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
       const int r = idx / KD, col = idx % KD;
-      Ws[r * WP + col] = r < len ? wb_[(t0 + r) * p.sw_t + col] : 0.f;
-      Ks[r * WP + col] = r < len ? kb_[(t0 + r) * p.sk_t + col] : 0.f;
+      Ws[r * WP + col] = r < len ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
+      Ks[r * WP + col] = r < len ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
     }
     for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
       const int r = idx / VT, col = idx % VT;
-      Us[r * UP + col] = r < len ? ub_[(t0 + r) * p.su_t + col] : 0.f;
+      Us[r * UP + col] = r < len ? (float)ub_[(t0 + r) * p.su_t + col] : 0.f;
     }
     if (threadIdx.x < 64) {
       const int t = threadIdx.x;
@@ -975,23 +1001,31 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       float gamma = t < len ? 1.f : 0.f, a = 1.f;
       if (gb_ != nullptr) {
         const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
-        gamma = t < len ? safe_exp(glast - gv) : 0.f;
-        a = expf(glast);
+        if constexpr (CONTEST) {
+          // fp16 gate of every token and fp16 exp of the fp16 g_last (generate_golden.py:409-416)
+          gamma = t < len ? f16_sat(expf(glast - gv)) : 0.f;
+          a = (float)(_Float16)expf(f16_sat(glast));
+        } else {
+          gamma = t < len ? safe_exp(glast - gv) : 0.f;
+          a = expf(glast);
+        }
+      } else if constexpr (CONTEST) {
+        a = 1.f;   // exp(0) in every precision
       }
       Gs[t] = gamma;
       if (t == 0) Gs[64] = a;
     }
     __syncthreads();
 
-    // h snapshot (fp32, exact)
+    // h snapshot (exact: fp32, or the bf16 state in contest mode)
     {
-      float* hdst = hb_ + (tk.boh + c) * p.sh_c;
+      E* hdst = hb_ + (tk.boh + c) * p.sh_c;
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-          hdst[(int64_t)krow * p.V + vcol] = S[kt][r];
+          hdst[(int64_t)krow * p.V + vcol] = (E)S[kt][r];
         }
     }
     // MM1: acc[tt] = W S   (contraction slot g of step (kt, r) is k = pi(kt, 4g + r))
@@ -1016,22 +1050,41 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-        const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
-        if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
-        Vd[tt][r] = vn * Gs[t];
+        if constexpr (CONTEST) {
+          const float ws = f16_nan_to_num(bf16_rnd(acc[tt][r]));
+          const float v16 = f16_sat(f16_sat(Us[t * UP + 16 * wave + n]) - ws);
+          if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = (E)v16;
+          Vd[tt][r] = t < len ? bf16_rnd(f16_sat(v16 * Gs[t])) : 0.f;
+        } else {
+          const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
+          if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+          Vd[tt][r] = vn * Gs[t];
+        }
       }
-    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r))
+    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r));
+    // contest mode: the update is its own bf16 GEMM, combined with the decayed state in bf16
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      S[kt] = S[kt] * a;
+      f32x4 up;
+      if constexpr (CONTEST) up = f32x4{0.f, 0.f, 0.f, 0.f};
+      else up = S[kt] * a;
       const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-          S[kt] = mfma_f32(Ks[t * WP + krow], Vd[tt][r], S[kt]);
+          up = mfma_f32(Ks[t * WP + krow], Vd[tt][r], up);
         }
+      if constexpr (CONTEST) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float hd = f16_sat(f16_sat(S[kt][r]) * a);
+          S[kt][r] = bf16_rnd(bf16_rnd(hd) + bf16_rnd(f16_nan_to_num(bf16_rnd(up[r]))));
+        }
+      } else {
+        S[kt] = up;
+      }
     }
   }
   if (p.final_state != nullptr) {

@@ -65,6 +65,18 @@ typedef enum cgdr_dtype {
   CGDR_F32 = 1
 } cgdr_dtype;
 
+/* Rounding model of the recurrence (cgdr_fwd_h_args.numerics).
+ *   CGDR_NUMERICS_DEFAULT: bf16 inputs follow the Triton kernel (docs/problem.txt:330-432):
+ *     fp32 state, bf16(S) and bf16(gated v_new) as GEMM operands; fp32 inputs are exact fp32.
+ *   CGDR_NUMERICS_CONTEST: bf16 inputs only; the contest reference run() /
+ *     run_reference (docs/problem.txt:81-167, code/tests/golden/generate_golden.py:350-440):
+ *     bf16 state, bf16 GEMM outputs, saturating fp16 casts and nan_to_num after each GEMM.
+ *     A simpler, slower kernel (not the pipelined one). */
+typedef enum cgdr_numerics {
+  CGDR_NUMERICS_DEFAULT = 0,
+  CGDR_NUMERICS_CONTEST = 1
+} cgdr_numerics;
+
 /* Arguments of one FwdH call.  Field meaning follows the Triton wrapper
  * (docs/problem.txt:436-472): k [B,T,Hg,K], w [B,T,H,K], u [B,T,H,V], g [B,T,H],
  * initial_state [N,H,K,V] -> h [B,NT,H,K,V], v_new [B,T,H,V], final_state [N,H,K,V]. */
@@ -88,7 +100,7 @@ typedef struct cgdr_fwd_h_args {
   int32_t in_dtype;             /* cgdr_dtype of k, w, u, h, v_new                        */
   int32_t h0_dtype;             /* cgdr_dtype of initial_state                            */
   int32_t final_dtype;          /* cgdr_dtype of final_state                              */
-  int32_t reserved0;
+  int32_t numerics;             /* cgdr_numerics (0 = CGDR_NUMERICS_DEFAULT)              */
 
   /* element strides of the outer dimensions */
   int64_t stride_k[3];          /* (b, t, key head)                                        */
@@ -121,7 +133,7 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace,
  * Exposed for tests and benchmarks; the reference's counterpart is the tiling data
  * written by ChunkGatedDeltaRuleFwdHTilingFunc (code/op_host/chunk_gated_delta_rule_fwd_h_tiling.cpp:152-261). */
 typedef struct cgdr_fwd_h_plan {
-  int32_t kernel;       /* 0: bf16 MFMA pipeline, 1: fp32 MFMA kernel                */
+  int32_t kernel;       /* 0: bf16 MFMA pipeline, 1: fp32 MFMA kernel, 2: contest numerics */
   int32_t v_tile;       /* value columns per workgroup                               */
   int32_t compute_waves;/* 64-lane waves doing MFMA work per workgroup               */
   int32_t total_waves;  /* waves per workgroup (compute + load/store)                */

@@ -24,6 +24,11 @@ What it restates (paths relative to the reference's
   placement of these rounding points is restated from the kernel text, which cannot run
   here; the tests pin ``bf16_round`` bit for bit against torch and the rounded loop only to
   within bf16 tolerance of the exact one.
+* ``fwd_h_o2`` -- the contest reference ``run()`` / the golden generator's
+  ``run_reference`` ("O2", ``code/tests/golden/generate_golden.py:350-440``,
+  ``docs/problem.txt:81-167``): bf16 state, bf16 GEMM outputs, saturating fp16 casts
+  (``cast_to_float16``, ``generate_golden.py:285-290``) and ``nan_to_num`` after each GEMM.
+  Pinned by the reference's own golden cases (``tests/golden/cases``).
 * ``prepare_chunk_offsets`` / ``prepare_chunk_indices`` -- ``docs/problem.txt:251-270``
   and ``code/tests/golden/generate_golden.py:260-282``.
 * ``safe_exp`` -- ``docs/problem.txt:272-274``.
@@ -238,6 +243,68 @@ def fwd_h(
             S = S + np.matmul(np.transpose(Kc, (0, 2, 1)), Vd)
         if output_final_state:
             final[n] = S
+    return h_out, v_out, final
+
+
+# ----------------------------------------------------------------------------- O2 (contest run())
+
+def f16_sat(x: np.ndarray) -> np.ndarray:
+    """``cast_to_float16`` (``code/tests/golden/generate_golden.py:285-290``): round to fp16;
+    finite inputs that overflow saturate to +-65504, inf and NaN pass through."""
+    x = np.asarray(x, np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        h = x.astype(np.float16)
+    special = ~np.isfinite(x)
+    return np.where(special, h, np.clip(h, np.float16(-65504), np.float16(65504))).astype(np.float16)
+
+
+def f16_nan_to_num(x: np.ndarray) -> np.ndarray:
+    """``torch.nan_to_num(x.to(float16), nan=0, posinf=inf, neginf=-inf)``."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        h = np.asarray(x, np.float32).astype(np.float16)
+    return np.where(np.isnan(h), np.float16(0), h).astype(np.float16)
+
+
+def fwd_h_o2(k, w, u, g, initial_state=None, cu_seqlens=None, chunk_size: int = CHUNK_SIZE):
+    """O2: the golden generator's ``run_reference`` (``generate_golden.py:350-440``), in its
+    head-major layouts: k ``[1,T,HK,K]``, w ``[1,HV,T,K]``, u ``[1,HV,T,V]``, g ``[1,HV,T]``,
+    initial_state ``[N,HV,K,V]`` -> h ``[1,HV,NT,K,V]``, v ``[1,HV,T,V]``, final ``[N,HV,K,V]``,
+    all bf16 values (float32 arrays).  A bf16 GEMM is a float32 product rounded once to bf16
+    (``ws = w_sel @ state``, ``update = k^T @ v_decay_bf16``, ``:397``, ``:423``)."""
+    k = np.asarray(k, np.float32)
+    w = np.asarray(w, np.float32)
+    u = np.asarray(u, np.float32)
+    g = np.asarray(g, np.float32)
+    _, T, HK, K = k.shape
+    HV, V = u.shape[1], u.shape[3]
+    cu = np.array([0, T]) if cu_seqlens is None else np.asarray(cu_seqlens, np.int64)
+    offs = prepare_chunk_offsets(cu, chunk_size)
+    N, NT = len(cu) - 1, int(offs[-1])
+    ratio = HV // HK
+    h_out = np.zeros((1, HV, NT, K, V), np.float32)
+    v_out = np.zeros((1, HV, T, V), np.float32)
+    final = np.zeros((N, HV, K, V), np.float32)
+    f32 = lambda x: np.asarray(x, np.float32)
+    for n in range(N):
+        bos, eos = int(cu[n]), int(cu[n + 1])
+        for hh in range(HV):
+            S = np.zeros((K, V), np.float32) if initial_state is None else bf16_round(initial_state[n, hh])
+            for c, t0 in enumerate(range(bos, eos, chunk_size)):
+                t1 = min(t0 + chunk_size, eos)
+                h_out[0, hh, int(offs[n]) + c] = S
+                ks = k[0, t0:t1, hh // ratio]
+                ws = bf16_round(w[0, hh, t0:t1] @ S)
+                v16 = f16_sat(f32(f16_sat(u[0, hh, t0:t1])) - f32(f16_nan_to_num(ws)))
+                gs = g[0, hh, t0:t1]
+                gate = f16_sat(np.exp(gs[-1] - gs))
+                vd = bf16_round(f32(f16_sat(f32(v16) * f32(gate)[:, None])))
+                with np.errstate(over="ignore"):
+                    sg = np.exp(f32(f16_sat(gs[-1:]))).astype(np.float16)
+                hd16 = f16_sat(f32(f16_sat(S)) * f32(sg))
+                upd16 = f16_nan_to_num(bf16_round(ks.T @ vd))
+                S = bf16_round(f32(bf16_round(f32(hd16))) + f32(bf16_round(f32(upd16))))
+                v_out[0, hh, t0:t1] = bf16_round(f32(v16))
+            final[n, hh] = S
     return h_out, v_out, final
 
 

@@ -26,7 +26,8 @@ def lib():
 def test_exports_every_declared_symbol(lib):
     inc = os.path.dirname(HEADER)
     text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
-    declared = set(re.findall(r"\b(cgdr_[a-z0-9_]+)\s*\(", text))
+    # function declarations: a return type at the start of a line, then the name and "("
+    declared = set(re.findall(r"^(?:cgdr_status|const char\s*\*|int)\s+(cgdr_[a-z0-9_]+)\s*\(", text, re.M))
     assert declared == set(_abi.EXPORTED_SYMBOLS)
     for name in declared:
         assert hasattr(lib, name), name
@@ -50,7 +51,7 @@ int main(void) {
   F(cgdr_chunk_o_args, o); F(cgdr_chunk_o_args, chunk_size); F(cgdr_chunk_o_args, scale);
   F(cgdr_chunk_o_args, in_dtype); F(cgdr_chunk_o_args, stride_q); F(cgdr_chunk_o_args, stride_o);
   F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
-  F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, reserved0); F(cgdr_fwd_h_args, stride_k);
+  F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, numerics); F(cgdr_fwd_h_args, stride_k);
   F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final);
   F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups);
   return 0;
