@@ -237,7 +237,7 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.has_g = a->g != nullptr;
   p.prefetch = env_int("CGDR_FWD_H_PREFETCH", 4);
   p.helpers = pl.helpers;
-  p.helper_lead = env_int("CGDR_FWD_H_HELPER_LEAD", 8);
+  p.helper_lead = env_int("CGDR_FWD_H_HELPER_LEAD", 4);
   {
     int hw = env_int("CGDR_FWD_H_HELPER_WAVES", 4);
     const int max_hw = pl.threads / 64;

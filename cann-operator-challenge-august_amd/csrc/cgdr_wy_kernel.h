@@ -14,12 +14,15 @@
 // Phases, separated by workgroup barriers:
 //   0  DMA of the k and v tiles into LDS; wave 0 forms g (each lane sums a_0..a_i in order,
 //      which is the sequential cumsum bit for bit), beta e^g and beta
-//   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, k rows straight from HBM/L2),
+//   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, operands read from the k tile),
 //      A written to LDS in fp32
 //   2  T: wave 0 inverts the four 16x16 diagonal blocks by forward substitution (lane = block,
-//      column); then T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj block by block in three levels
-//      (block distance 1, 2, 3) with fp32 MFMA 16x16x4.  The contraction slot of lane group G at
-//      step kk is 4 G + kk, so a C-layout result is directly the B operand of the next product.
+//      column; each solved row updates the partial sums of all later rows at once, so the
+//      dependent chain is 16 steps); then T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj block by block in
+//      three levels (block distance 1, 2, 3) with fp32 MFMA 16x16x4.  The contraction slot of
+//      lane group G at step kk is 4 G + kk, so a C-layout result is directly the B operand of the
+//      next product.  A and T share one fp32 matrix M: A_ij = M[i][j] below the diagonal, T is
+//      stored transposed, T_ij = M[j][i] on and above it (T's upper triangle is zero).
 //   3  w^T = k^T T'^T and u^T = v^T T''^T with bf16 MFMA: the A operands are transposed reads of
 //      the k / v tiles, the B operands rows of T scaled per column and rounded to bf16; each lane
 //      ends with 8 consecutive columns of one token, written with 16-byte stores.
@@ -56,9 +59,8 @@ struct WyLayout {
   static constexpr int MS = 68;                    // fp32 row stride of A and T (conflict-free columns)
   static constexpr int K_OFF = 0;                  // k tile [64][KD] bf16
   static constexpr int V_OFF = 64 * KD * 2;        // v tile [64][VD] bf16
-  static constexpr int A_OFF = V_OFF + 64 * VD * 2;
-  static constexpr int T_OFF = A_OFF + 64 * MS * 4;
-  static constexpr int G_OFF = T_OFF + 64 * MS * 4;   // g [64], beta e^g [64], beta [64], a [64]
+  static constexpr int M_OFF = V_OFF + 64 * VD * 2;   // A (strictly lower) and T^T (upper), fp32
+  static constexpr int G_OFF = M_OFF + 64 * MS * 4;   // g [64], beta e^g [64], beta [64], a [64]
   static constexpr int LDS_BYTES = G_OFF + 4 * 256;
   static constexpr int RPDK = 64 / PK, RPDV = 64 / PV;
   static constexpr int DMA_K = 64 / RPDK, DMA_V = 64 / RPDV;
@@ -116,20 +118,6 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
         *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
     }
   }
-  // k rows for S = k k^T: rows j = 16 t + n (t <= wave) and this wave's columns i = 16 wave + n
-  // (a separate copy, so that no register array is indexed by the wave number)
-  const u32x4 zero4 = {0, 0, 0, 0};
-  u32x4 kf[4][KS], kc[KS];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int j = 16 * t + n;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kf[t][ks] = (t <= wave && j < len) ? *(const u32x4*)(kb + j * p.sk_t + 32 * ks + 8 * G) : zero4;
-  }
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks)
-    kc[ks] = 16 * wave + n < len ? *(const u32x4*)(kb + (16 * wave + n) * p.sk_t + 32 * ks + 8 * G) : zero4;
   float* GA = (float*)(smem + L::G_OFF);
   if (wave == 0) {
     float bt = 0.f, at = 0.f;
@@ -158,19 +146,25 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   wait_lgkm0();
   block_barrier();
 
-  // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i); lane holds S[16t + 4G + r][i]
-  float* Am = (float*)(smem + L::A_OFF);
-  float* Tm = (float*)(smem + L::T_OFF);
+  // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i); lane holds S[16t + 4G + r][i].
+  // Operands are k rows from the tile: row j, contraction slice 32 ks + 8 G .. +7 (one piece).
+  float* M = (float*)(smem + L::M_OFF);
   const int i = 16 * wave + n;
+  const lds_char* ktile = (const lds_char*)smem + L::K_OFF;
+  auto krow = [&](int j, int ks) {
+    return __builtin_bit_cast(bf16x8, *(const u32x4*)(ktile + (j * L::PK + ((4 * ks + G) ^ swz_k<L::PK>(j))) * 16));
+  };
   {
     const float gi = GA[i], bi = GA[128 + i];
+    bf16x8 kc[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kc[ks] = krow(i, ks);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       if (t > wave) continue;
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        c = mfma_bf16(__builtin_bit_cast(bf16x8, kf[t][ks]), __builtin_bit_cast(bf16x8, kc[ks]), c);
+      for (int ks = 0; ks < KS; ++ks) c = mfma_bf16(krow(16 * t + n, ks), kc[ks], c);
       const f32x4 gj = *(const f32x4*)(GA + 16 * t + 4 * G);
       f32x4 a;
 #pragma unroll
@@ -178,63 +172,67 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
         const int j = 16 * t + 4 * G + r;
         a[r] = j < i ? bi * c[r] * expf(gi - gj[r]) : 0.f;
       }
-      *(f32x4*)(Am + i * MS + 16 * t + 4 * G) = a;
+      *(f32x4*)(M + i * MS + 16 * t + 4 * G) = a;
     }
   }
   wait_lgkm0();
   block_barrier();
 
-  // ---- phase 2a: diagonal blocks T_bb = (I + A_bb)^{-1}, lane = (block bb, column c)
+  // T_rc (r >= c) lives at M[c][r]; entries above T's diagonal read as zero
+  auto tval = [&](int r, int c) { return r >= c ? M[c * MS + r] : 0.f; };
+
+  // ---- phase 2a: diagonal blocks T_bb = (I + A_bb)^{-1}, lane = (block bb, column c).
+  // acc[r] collects 1_{r=c} - sum_{j<r} A_rj T_jc in the order j = 0, 1, ..., r-1.
   if (wave == 0) {
-    const int bb = lane >> 4, c = lane & 15;
-    float tcol[16];
+    const int bb = lane >> 4, c = lane & 15, o = 16 * bb;
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = r == c ? 1.f : 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float* arow = Am + (16 * bb + r) * MS + 16 * bb;
-      float acc = r == c ? 1.f : 0.f;
 #pragma unroll
-      for (int j = 0; j < r; ++j) acc -= arow[j] * tcol[j];
-      tcol[r] = acc;
+      for (int r2 = r + 1; r2 < 16; ++r2) acc[r2] -= M[(o + r2) * MS + o + r] * acc[r];
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) Tm[(16 * bb + r) * MS + 16 * bb + c] = tcol[r];
+    for (int r = 0; r < 16; ++r)
+      if (r >= c) M[(o + c) * MS + o + r] = acc[r];
   }
   wait_lgkm0();
   block_barrier();
 
   // ---- phase 2b: off-diagonal blocks, one level per block distance
-  // acc += X[xr.., xc..] Y[yr.., yc..] (16x16 blocks of LDS matrices)
-  auto mm = [&](f32x4 acc, const float* X, int xr, int xc, const float* Y, int yr, int yc) {
+  // acc += A[xr.., xc..] T[yr.., yc..] (16x16 blocks; A below the diagonal, T diagonal or below)
+  auto mm = [&](f32x4 acc, int xr, int xc, int yr, int yc) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk)
-      acc = mfma_f32(X[(xr + n) * MS + xc + 4 * G + kk], Y[(yr + 4 * G + kk) * MS + yc + n], acc);
+      acc = mfma_f32(M[(xr + n) * MS + xc + 4 * G + kk], tval(yr + 4 * G + kk, yc + n), acc);
     return acc;
   };
-  // -(X[xr.., xc..] Y) stored into T[tr.., tc..], Y held in C layout
+  // T[tr.., tc..] = -(T_{tr,tr} Y), Y held in C layout
   auto finish = [&](const f32x4& Y, int tr, int tc) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) acc = mfma_f32(Tm[(tr + n) * MS + tr + 4 * G + kk], Y[kk], acc);
+    for (int kk = 0; kk < 4; ++kk) acc = mfma_f32(tval(tr + n, tr + 4 * G + kk), Y[kk], acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) Tm[(tr + 4 * G + r) * MS + tc + n] = -acc[r];
+    for (int r = 0; r < 4; ++r) M[(tc + n) * MS + tr + 4 * G + r] = -acc[r];
   };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   if (wave >= 1) {   // distance 1: T_{w,w-1} = -T_ww A_{w,w-1} T_{w-1,w-1}
     const int bi = 16 * wave, bj = 16 * (wave - 1);
-    finish(mm(z4, Am, bi, bj, Tm, bj, bj), bi, bj);
+    finish(mm(z4, bi, bj, bj, bj), bi, bj);
   }
   wait_lgkm0();
   block_barrier();
   if (wave >= 2) {   // distance 2: T_{w,w-2} = -T_ww (A_{w,w-2} T_{w-2,w-2} + A_{w,w-1} T_{w-1,w-2})
     const int bi = 16 * wave, bj = 16 * (wave - 2), bk = 16 * (wave - 1);
-    finish(mm(mm(z4, Am, bi, bj, Tm, bj, bj), Am, bi, bk, Tm, bk, bj), bi, bj);
+    finish(mm(mm(z4, bi, bj, bj, bj), bi, bk, bk, bj), bi, bj);
   }
   wait_lgkm0();
   block_barrier();
   if (wave == 3) {   // distance 3: T_30 = -T_33 (A_30 T_00 + A_31 T_10 + A_32 T_20)
-    f32x4 x = mm(z4, Am, 48, 0, Tm, 0, 0);
-    x = mm(x, Am, 48, 16, Tm, 16, 0);
-    x = mm(x, Am, 48, 32, Tm, 32, 0);
+    f32x4 x = mm(z4, 48, 0, 0, 0);
+    x = mm(x, 48, 16, 16, 0);
+    x = mm(x, 48, 32, 32, 0);
     finish(x, 48, 0);
   }
   wait_lgkm0();
@@ -251,20 +249,18 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
     float tw[8], tu[8];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const f32x4 t4 = *(const f32x4*)(Tm + i * MS + j0 + 4 * h);
       const f32x4 sg = *(const f32x4*)(GA + 64 + j0 + 4 * h);
       const f32x4 sb = *(const f32x4*)(GA + 128 + j0 + 4 * h);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const bool in = j0 + 4 * h + r <= i;
-        tw[4 * h + r] = in ? t4[r] * sg[r] : 0.f;
-        tu[4 * h + r] = in ? t4[r] * sb[r] : 0.f;
+        const float t = tval(i, j0 + 4 * h + r);
+        tw[4 * h + r] = t * sg[r];
+        tu[4 * h + r] = t * sb[r];
       }
     }
     bw[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
     bu[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
   }
-  const lds_char* ktile = (const lds_char*)smem + L::K_OFF;
   const lds_char* vtile = (const lds_char*)smem + L::V_OFF;
   const bool store = i < len;
 #pragma unroll
