@@ -162,7 +162,9 @@ def chunk_gated_delta_rule_fwd_h(
     if g is not None:
         if tuple(g.shape) != (B, T, H):
             raise ValueError(f"g must have shape [B,T,H]={[B, T, H]}, got {list(g.shape)}")
-        g = g.float().contiguous() if g.dtype != torch.float32 or g.stride(-1) != 1 else g
+        # any strides: the library reads g in place when its token stride is 1 (e.g. a
+        # head-major buffer) and copies it head-major into the workspace otherwise
+        g = g.float() if g.dtype != torch.float32 else g
     dev = k.device
     if cu_seqlens is None:
         if chunk_indices is not None or chunk_offsets is not None:

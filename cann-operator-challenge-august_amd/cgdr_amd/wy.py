@@ -32,7 +32,8 @@ def wy_fwd(
     chunk_indices: torch.Tensor | None = None,
     chunk_size: int = CHUNK_SIZE,
 ):
-    """``(w [B,T,H,K], u [B,T,H,V], g_cumsum [B,T,H] fp32)``; bf16 k and v."""
+    """``(w [B,T,H,K], u [B,T,H,V], g_cumsum [B,T,H] fp32)``; bf16 k and v.  g_cumsum is a
+    head-major view (strides ``(H*T, 1, T)``)."""
     if chunk_size != CHUNK_SIZE:
         raise ValueError(f"chunk_size must be {CHUNK_SIZE}, but got {chunk_size}")
     for t, name in ((k, "k"), (v, "v")):
@@ -68,7 +69,10 @@ def wy_fwd(
     k, v = _prep_input(k, "k", 16), _prep_input(v, "v", 16)
     w = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev)
     u = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=dev)
-    gc = torch.zeros(B, T, H, dtype=torch.float32, device=dev)
+    # g_cumsum is stored head-major ([B,H,T] memory, returned as a [B,T,H] view): every token
+    # belongs to a chunk, so the kernel writes all of it, and FwdH and the chunk output read
+    # one chunk's gate row of one head as 256 contiguous bytes (no relayout in FwdH)
+    gc = torch.empty(B, H, T, dtype=torch.float32, device=dev).transpose(1, 2)
     a = _abi.WyArgs()
     a.k, a.v, a.beta, a.g = k.data_ptr(), v.data_ptr(), beta.data_ptr(), _ptr(g)
     a.cu_seqlens, a.chunk_indices = _ptr(cu_dev), _ptr(ci_dev)
