@@ -3,7 +3,7 @@
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--op fwd_h|chunk_o|wy|forward]
 
 A step is one FwdH call over the long-context prefill workload
-B=1, T=32768, H=Hg=32, K=V=128, bf16 k/w/u, fp32 g, h0=None, final state on
+B=1, T=32768, H=Hg=32, K=V=128, bf16 k/w/u, fp32 g (head-major), h0=None, final state on
 (512 chunks per sequence walked inside the kernel).  Inputs are synthetic (seeded, the
 distributions of the CPU-runnable reference case) and resident in HBM before timing.
 Prints one JSON line: whole-job tokens/s, the dominant kernel's achieved HBM bandwidth
@@ -48,7 +48,8 @@ def algorithmic_flops(B, NT, H, K, V):
 
 def make_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
     """Synthetic inputs on the device: k L2-normalised randn, w = randn K^-1/2, u = randn,
-    g = chunk-local cumsum of logsigmoid(randn) (non-increasing, <= 0 within each chunk)."""
+    g = chunk-local cumsum of logsigmoid(randn) (non-increasing, <= 0 within each chunk),
+    stored head-major."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(seed)
     k = torch.randn(B, T, Hg, K, device=dev, generator=gen)
@@ -59,7 +60,10 @@ def make_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
     NT = (T + 63) // 64
     pad = NT * 64 - T
     inc = torch.nn.functional.pad(inc, (0, 0, 0, pad)).view(B, NT, 64, H)
-    g = inc.cumsum(dim=2).view(B, NT * 64, H)[:, :T].contiguous()
+    g = inc.cumsum(dim=2).view(B, NT * 64, H)[:, :T]
+    # g stored head-major ([B,H,T] memory, the layout of the contest run() and of the WY
+    # producer's output), passed as a [B,T,H] view: the library reads it in place
+    g = g.transpose(1, 2).contiguous().transpose(1, 2)
     return k, w, u, g
 
 
