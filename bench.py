@@ -321,6 +321,8 @@ def main():
     ap.add_argument("--op", choices=("fwd_h", "chunk_o", "wy", "forward"), default="fwd_h",
                     help="fwd_h: the headline FwdH step (default); chunk_o: the chunk output; wy: the WY "
                          "producer; forward: WY -> FwdH -> chunk output")
+    ap.add_argument("--numerics", choices=("default", "contest"), default="default",
+                    help="fwd_h rounding model: default (the Triton kernel's) or contest (run()'s casts)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 elementwise copy (the reference kernel of known "
                          "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -357,7 +359,7 @@ def main():
     progress("fwd_h inputs resident in HBM")
 
     def step():
-        return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, output_final_state=True)
+        return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, output_final_state=True, numerics=args.numerics)
 
     for _ in range(args.warmup):
         step()
@@ -406,7 +408,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "ChunkGatedDeltaRuleFwdH long-context prefill", **W,
-                   "h0": None, "output_final_state": True, "parallelism": "none (1 GPU)"},
+                   "h0": None, "output_final_state": True, "numerics": args.numerics,
+                   "parallelism": "none (1 GPU)"},
         "hbm_gbps": achieved,
         "kernel_ms": avg_ms,
         "kernel_ms_min": min(kern_ms),

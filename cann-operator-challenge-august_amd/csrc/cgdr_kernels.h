@@ -986,14 +986,34 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     const int64_t t0 = tk.bos + (int64_t)c * kChunk;
     const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
-      const int r = idx / KD, col = idx % KD;
-      Ws[r * WP + col] = r < len ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
-      Ks[r * WP + col] = r < len ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
-    }
-    for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
-      const int r = idx / VT, col = idx % VT;
-      Us[r * UP + col] = r < len ? (float)ub_[(t0 + r) * p.su_t + col] : 0.f;
+    if constexpr (CONTEST) {
+      // bf16 rows are 16-byte aligned (checked on the host): 8 elements per load
+      auto widen = [](const u32x4& x, float* dst) {
+        const f32x4 lo = {bf16_lo(x[0]), bf16_hi(x[0]), bf16_lo(x[1]), bf16_hi(x[1])};
+        const f32x4 hi = {bf16_lo(x[2]), bf16_hi(x[2]), bf16_lo(x[3]), bf16_hi(x[3])};
+        *(f32x4*)dst = lo;
+        *(f32x4*)(dst + 4) = hi;
+      };
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      for (int idx = threadIdx.x; idx < 64 * KD / 8; idx += L::THREADS) {
+        const int r = idx / (KD / 8), col = 8 * (idx % (KD / 8));
+        widen(r < len ? *(const u32x4*)(wb_ + (t0 + r) * p.sw_t + col) : z, Ws + r * WP + col);
+        widen(r < len ? *(const u32x4*)(kb_ + (t0 + r) * p.sk_t + col) : z, Ks + r * WP + col);
+      }
+      for (int idx = threadIdx.x; idx < 64 * VT / 8; idx += L::THREADS) {
+        const int r = idx / (VT / 8), col = 8 * (idx % (VT / 8));
+        widen(r < len ? *(const u32x4*)(ub_ + (t0 + r) * p.su_t + col) : z, Us + r * UP + col);
+      }
+    } else {
+      for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
+        const int r = idx / KD, col = idx % KD;
+        Ws[r * WP + col] = r < len ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
+        Ks[r * WP + col] = r < len ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
+      }
+      for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
+        const int r = idx / VT, col = idx % VT;
+        Us[r * UP + col] = r < len ? (float)ub_[(t0 + r) * p.su_t + col] : 0.f;
+      }
     }
     if (threadIdx.x < 64) {
       const int t = threadIdx.x;
