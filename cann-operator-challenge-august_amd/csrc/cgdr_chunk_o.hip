@@ -26,6 +26,8 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // V-tile: 128 value columns when V allows it (and K <= 128, which keeps the LDS of one
 // workgroup at 48 KiB so three fit a CU), else 64, else 32.
 int pick_vtile(const cgdr_chunk_o_args* a) {
+  const int forced = cgdr_host::env_int("CGDR_CHUNK_O_VTILE", 0);
+  if ((forced == 32 || forced == 64 || (forced == 128 && a->K <= 128)) && a->V % forced == 0) return forced;
   if (a->V % 128 == 0 && a->K <= 128) return 128;
   if (a->V % 64 == 0) return 64;
   if (a->V % 32 == 0) return 32;
