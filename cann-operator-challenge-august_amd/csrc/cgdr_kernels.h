@@ -23,12 +23,12 @@
 // Roles inside a workgroup (wave index):
 //   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
 //   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
-//               c+STAGES-1 (shared round-robin); wave 0 also moves the g row one chunk
-//               further ahead
+//               c+STAGES-1 (shared round-robin)
 //   NCW+NLW .. NCW+NLW+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1
-//               from LDS staging to HBM, store instructions shared round-robin
-//   NCW+NLW+NSW gate/prefetch wave: gate factors of chunk c+1 into LDS, and touches chunk
-//               c+prefetch into L2
+//               from LDS staging to HBM, store instructions shared round-robin; without
+//               helper workgroups, store wave 0 also touches chunk c+prefetch into L2
+//   NCW+NLW+NSW gate wave: loads the raw g rows (two chunks ahead, into registers) and
+//               writes the gate factors of chunk c+1 into LDS
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
 #pragma once
@@ -258,8 +258,7 @@ struct Bf16Layout {
   static constexpr int K_OFF = 128 * KD;
   static constexpr int U_OFF = 256 * KD;
   static constexpr int G_OFF = 256 * KD + 128 * VT;            // gamma[64], a
-  static constexpr int GRAW_OFF = G_OFF + 512;                  // raw g row of the chunk
-  static constexpr int STAGE_BYTES = ((GRAW_OFF + 256) + 255) / 256 * 256;
+  static constexpr int STAGE_BYTES = ((G_OFF + 260) + 255) / 256 * 256;
   static constexpr int SS_OFF = STAGES * STAGE_BYTES;          // state staging, 2 buffers
   static constexpr int SS_BYTES = VT * KD * 2;
   static constexpr int SV_OFF = SS_OFF + 2 * SS_BYTES;         // v_new staging, 2 buffers
@@ -272,10 +271,10 @@ struct Bf16Layout {
   static constexpr int DMA_U = (128 * VT + 1023) / 1024;
   static constexpr int DMA_TILES = 2 * DMA_W + DMA_U;         // per chunk, over all load waves
   // DMA instructions load wave lw issues per full chunk: tile instruction i goes to wave
-  // i % NLW, and wave 0 also moves the g row.
+  // i % NLW.
   template <int LW>
   static constexpr int dma_per_chunk() {
-    return DMA_TILES / NLW + (LW < DMA_TILES % NLW ? 1 : 0) + (LW == 0 ? 1 : 0);
+    return DMA_TILES / NLW + (LW < DMA_TILES % NLW ? 1 : 0);
   }
 };
 
@@ -323,16 +322,15 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   const int hk = tk.head / p.head_ratio;
   const bool has_g = p.g != nullptr;
 
-  // Gate factors of chunk c into stage st from its raw g row (one wave):
-  // gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows, and a = exp(g_last) in
-  // slot 64.  No gating: gamma = 1, a = 1.
-  auto gates = [&](int c, int st) {
+  // Gate factors of chunk c into stage st from its raw g row (one wave; gv = g of token
+  // `lane` of the chunk): gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows,
+  // and a = exp(g_last) in slot 64.  No gating: gamma = 1, a = 1.
+  auto gates = [&](int c, int st, float gv) {
     const int64_t rem = tk.len - (int64_t)c * kChunk;
     const int len = rem < kChunk ? (int)rem : kChunk;
     float* gdst = (float*)(smem + st * L::STAGE_BYTES + L::G_OFF);
     float gamma, a;
     if (has_g) {
-      const float gv = ((const float*)(smem + st * L::STAGE_BYTES + L::GRAW_OFF))[lane];
       const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
       gamma = lane < len ? safe_exp(glast - gv) : 0.f;
       a = expf(glast);
@@ -348,8 +346,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   // segment per lane (a 4-byte DMA into a scratch LDS area; nothing waits on it until exit),
   // the segments shared round-robin among the head's V-tile tasks, so that the load waves'
   // DMAs of that chunk hit L2 rather than HBM.  Per-lane segment addresses are fixed here; a
-  // chunk only adds t0 * row stride.  Used by the gate/prefetch wave (touching a few chunks
-  // ahead of its own load waves) or, in helper mode, by the task's helper workgroup.
+  // chunk only adds t0 * row stride.  Used by store wave 0 when there are no helper
+  // workgroups, touching a few chunks ahead of the load waves.
   constexpr int PF_INSTR = 4;
   const char* lptr[PF_INSTR];
   int64_t lstride[PF_INSTR];
@@ -627,14 +625,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     // ------------------------------------------------------------------ load waves
     // The tile DMAs of a chunk are dealt round-robin over the NLW load waves (instruction
     // i goes to wave i % NLW), so each wave's vmcnt covers only its share and more loads are
-    // in flight per CU.  Load wave 0 also moves the raw g row of the NEXT chunk ahead of each
-    // chunk's tiles, so that the row of chunk c+2 has landed when chunk c+1 has, and the
-    // gate wave can turn it into gate factors during chunk c+1 without waiting on anything.
+    // in flight per CU.  The g rows are not theirs: the gate wave loads them into registers.
     const int lw = wave - NCW;
     const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
     const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
     const __bf16* ubase = (const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
-    const float* gbase = p.g == nullptr ? nullptr : p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h;
 
     // Per-lane byte offsets (within a chunk) of the 16-byte pieces each DMA instruction moves,
     // hoisted out of the chunk loop: instruction m, lane -> LDS piece 64m + lane = (row r,
@@ -660,24 +655,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const char* ksrc = (const char*)kbase;
     const char* usrc = (const char*)ubase;
     const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
-    const char* gsrc = has_g ? (const char*)gbase : (const char*)wbase;
-    const int64_t sgt = has_g ? p.sg_t * 4 : 0;
 
     // One load wave's schedule; LW is its index (compile-time, selects its DMA share).
     auto run_loader = [&](auto lw_tag) {
       constexpr int LW = decltype(lw_tag)::value;
-      // Raw g row of chunk j (wave 0) into the GRAW area of its stage; rows past the
-      // sequence end repeat the last row.  Without g the same instruction moves filler, so
-      // every chunk issues the same number of loads.
-      auto issue_g = [&](int j) {
-        const int64_t rem = tk.len - (int64_t)j * kChunk;
-        const int len = rem < kChunk ? (int)rem : kChunk;
-        const char* gchunk = gsrc + (tk.bos + (int64_t)j * kChunk) * sgt;
-        const uint32_t goff = (uint32_t)((lane < len ? lane : len - 1) * sgt);
-        dma_b32(gchunk, goff, lds0 + (uint32_t)((j % STAGES) * L::STAGE_BYTES + L::GRAW_OFF));
-      };
-      // Issue this wave's share of the W, K, U tiles of chunk c into stage st (on wave 0,
-      // preceded by the g row of chunk c+1).  Every load is a direct-to-LDS DMA written as
+      // Issue this wave's share of the W, K, U tiles of chunk c into stage st.  Every load is a direct-to-LDS DMA written as
       // inline asm: the compiler then tracks none of them, and the explicit in-order vmcnt
       // waits below are the only waits (its own tracking cannot express more than 63
       // outstanding loads and would drain the whole pipeline instead).  A partial (last) chunk takes a masked path: rows at or
@@ -692,9 +674,6 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         const char* wchunk = wsrc + t0 * stw;
         const char* kchunk = ksrc + t0 * stk;
         const char* uchunk = usrc + t0 * stu;
-        if constexpr (LW == 0) {
-          if (c + 1 < NC) issue_g(c + 1);
-        }
         if (len == kChunk) {
 #pragma unroll
           for (int m = 0; m < L::DMA_W; ++m)
@@ -738,14 +717,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       static_assert((D - 1) * PER_CHUNK <= 63, "prefetch depth exceeds the vmcnt range");
       constexpr int STEADY_VM = (D - 1) * PER_CHUNK;
 
-      // Prologue: g row 0, then chunks 0 .. D-1 issued; chunk 0 (with g rows 0 and 1) landed
-      // and gated here.  The gate wave gates chunk c+1 during loop iteration c.
+      // Prologue: chunks 0 .. D-1 issued; chunk 0 landed here.
       if (NC > 0) {
-        if constexpr (LW == 0) issue_g(0);
         for (int j = 0; j < D && j < NC; ++j) issue(j, j);
         if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
         else wait_vm<0>();
-        if constexpr (LW == 0) gates(0, 0);
       }
       wait_lgkm0();
       block_barrier();   // P
@@ -833,8 +809,19 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       }
     };
 
+    // Without helper workgroups, store wave 0 also touches chunk c+prefetch into L2
+    // (l2_touch) at the start of iteration c.  Nothing waits on those touches until exit.
+    const int pf = p.prefetch;
+    const bool touching = sw == 0 && pf > 0 && !p.helpers;
+    auto prefetch = [&](int j) {
+      if (!touching || j >= NC || tk.len - (int64_t)j * kChunk < kChunk) return;
+      l2_touch(j);
+    };
+    if (touching) l2_touch_setup();
+    for (int j = 1; j < pf; ++j) prefetch(j);
     block_barrier();   // P
     for (int c = 0; c < NC; ++c) {
+      prefetch(c + pf);
       if (c >= 1) store_chunk(c - 1);
       wait_lgkm0();
       block_barrier();   // B_c
@@ -843,26 +830,33 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
                            __HIP_MEMORY_SCOPE_AGENT);
     }
     if (NC > 0) store_chunk(NC - 1);
+    if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
   } else if (wave == NCW + NLW + L::NSW) {
-    // ------------------------------------------------------------------ gate/prefetch wave
-    // Gate factors of chunk c+1 during iteration c: its raw g row landed with chunk c+1's
-    // tiles, before barrier B_{c-1}, and the factors are read after barrier B_c.
-    // Without helper workgroups this wave also touches chunk c+prefetch into L2 (l2_touch).
-    const int pf = p.prefetch;
-    auto prefetch = [&](int j) {
-      if (pf <= 0 || p.helpers || j >= NC || tk.len - (int64_t)j * kChunk < kChunk) return;
-      l2_touch(j);
+    // ------------------------------------------------------------------ gate wave
+    // Loads the raw g rows itself, with ordinary loads into registers two chunks ahead, and
+    // turns them into the gate factors of chunk c+1 during iteration c (read by the compute
+    // waves after barrier B_c).  The row of chunk c+2 is issued before the factors of chunk
+    // c+1 are computed, so the only wait is for a load issued one iteration earlier.  Rows
+    // past the sequence end repeat its last row.  (Keeping the g rows out of the load waves'
+    // DMA stream matters: a 256-byte row in that stream cost as much as a quarter of a tile.)
+    const float* gsrc = has_g ? p.g + tk.b * p.sg_b + (int64_t)tk.head * p.sg_h : nullptr;
+    auto graw = [&](int j) -> float {
+      if (gsrc == nullptr || j >= NC) return 0.f;
+      const int64_t rem = tk.len - (int64_t)j * kChunk;
+      const int len = rem < kChunk ? (int)rem : kChunk;
+      return gsrc[(tk.bos + (int64_t)j * kChunk + (lane < len ? lane : len - 1)) * p.sg_t];
     };
-    if (pf > 0 && !p.helpers) l2_touch_setup();
-    for (int j = 1; j < pf; ++j) prefetch(j);
+    float g_next = graw(1);
+    if (NC > 0) gates(0, 0, graw(0));
+    wait_lgkm0();
     block_barrier();   // P
     for (int c = 0; c < NC; ++c) {
-      prefetch(c + pf);
-      if (c + 1 < NC) gates(c + 1, (c + 1) % STAGES);
+      const float g_after = graw(c + 2);
+      if (c + 1 < NC) gates(c + 1, (c + 1) % STAGES, g_next);
+      g_next = g_after;
       wait_lgkm0();
       block_barrier();   // B_c
     }
-    wait_vm<0>();   // the prefetch DMAs write this workgroup's LDS: drain them before exit
   }
 }
 

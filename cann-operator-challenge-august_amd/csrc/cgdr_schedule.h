@@ -3,10 +3,9 @@
 // The load wave keeps D chunks of loads in flight (D = pipeline stages - 1).  At loop
 // iteration c it first issues chunk c+D, then waits for chunk c+1 with s_waitcnt vmcnt(N),
 // which returns once at most N of its VMEM instructions are outstanding; loads complete in
-// issue order.  The instructions of chunk j form one group (load wave 0 also moves the g row
-// of chunk j+1 ahead of chunk j's tiles).  A group is full -- exactly PER_CHUNK instructions --
-// for every chunk but the last of the sequence, which may be partial (DMA instructions with no
-// valid row are skipped) and has no next g row, so it must never be among the groups a
+// issue order.  The instructions of chunk j form one group.  A group is full -- exactly
+// PER_CHUNK instructions -- for every chunk but the last of the sequence, which may be partial
+// (DMA instructions with no valid row are skipped), so it must never be among the groups a
 // non-zero N leaves outstanding.
 #pragma once
 
