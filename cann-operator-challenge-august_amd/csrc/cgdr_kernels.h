@@ -20,15 +20,19 @@
 // so lane group g of two adjacent tiles holds 8 consecutive k (or tokens), which is the
 // 8-element contraction slice the v_mfma_f32_16x16x32_bf16 B operand wants.
 //
-// Roles inside a workgroup (wave index):
+// Roles inside a workgroup (wave index; the waves of a workgroup are dealt to the CU's four
+// SIMDs in order, so waves w and w+4 share one):
 //   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
-//   NCW .. NCW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
+//   NCW .. NCW+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1 from LDS
+//               staging to HBM, store instructions shared round-robin; without helper
+//               workgroups, store wave 0 also touches chunk c+prefetch into L2
+//   NCW+NSW .. NCW+NSW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
 //               c+STAGES-1 (shared round-robin)
-//   NCW+NLW .. NCW+NLW+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1
-//               from LDS staging to HBM, store instructions shared round-robin; without
-//               helper workgroups, store wave 0 also touches chunk c+prefetch into L2
-//   NCW+NLW+NSW gate wave: loads the raw g rows (two chunks ahead, into registers) and
+//   NCW+NSW+NLW gate wave: loads the raw g rows (two chunks ahead, into registers) and
 //               writes the gate factors of chunk c+1 into LDS
+// With two compute waves the order puts the store waves on SIMDs of their own and the light
+// load and gate waves beside the compute waves (measured: 13 % faster than the store waves
+// beside the compute waves).
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
 #pragma once
@@ -621,12 +625,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
         }
     }
-  } else if (wave < NCW + NLW) {
+  } else if (wave >= NCW + L::NSW && wave < NCW + L::NSW + NLW) {
     // ------------------------------------------------------------------ load waves
     // The tile DMAs of a chunk are dealt round-robin over the NLW load waves (instruction
     // i goes to wave i % NLW), so each wave's vmcnt covers only its share and more loads are
     // in flight per CU.  The g rows are not theirs: the gate wave loads them into registers.
-    const int lw = wave - NCW;
+    const int lw = wave - NCW - L::NSW;
     const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
     const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
     const __bf16* ubase = (const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
@@ -748,12 +752,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       else if (lw == 2) run_loader(std::integral_constant<int, 2>{});
       else run_loader(std::integral_constant<int, 3>{});
     }
-  } else if (wave < NCW + NLW + L::NSW) {
+  } else if (wave >= NCW && wave < NCW + L::NSW) {
     // ------------------------------------------------------------------ store waves
     // h snapshot and v_new of a chunk, from the LDS staging buffers: each 16-lane block takes
     // units of (16 rows x 8 value columns); two transposed reads give a lane 8 consecutive
     // value columns of one row, stored as one 16-byte write.
-    const int sw = wave - NCW - NLW;   // this store wave takes store instructions m % NSW == sw
+    const int sw = wave - NCW;   // this store wave takes store instructions m % NSW == sw
     const int blk = lane >> 4, i = lane & 15;
     const int e = i >> 2, q = i & 3;
     __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
@@ -831,7 +835,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
     if (NC > 0) store_chunk(NC - 1);
     if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
-  } else if (wave == NCW + NLW + L::NSW) {
+  } else if (wave == NCW + L::NSW + NLW) {
     // ------------------------------------------------------------------ gate wave
     // Loads the raw g rows itself, with ordinary loads into registers two chunks ahead, and
     // turns them into the gate factors of chunk c+1 during iteration c (read by the compute
