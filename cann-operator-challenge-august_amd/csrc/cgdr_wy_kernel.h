@@ -16,12 +16,12 @@
 //      which is the sequential cumsum bit for bit), beta e^g and beta
 //   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, operands read from the k tile),
 //      A written to LDS in fp32
-//   2  T: wave 0 inverts the four 16x16 diagonal blocks by forward substitution (lane = block,
-//      column; each solved row updates the partial sums of all later rows at once, so the
-//      dependent chain is 16 steps); then T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj block by block in
-//      three levels (block distance 1, 2, 3) with fp32 MFMA 16x16x4.  The contraction slot of
-//      lane group G at step kk is 4 G + kk, so a C-layout result is directly the B operand of the
-//      next product.  A and T share one fp32 matrix M: A_ij = M[i][j] below the diagonal, T is
+//   2  T: each wave inverts its own 16x16 diagonal block by forward substitution right after
+//      writing its row block of A (lane = column; each solved row updates the partial sums of all
+//      later rows at once, so the dependent chain is 16 steps); after one barrier, wave j computes
+//      column block j, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i = j+1 .. 3 in order, with fp32
+//      MFMA 16x16x4 and no further barrier.  The contraction slot of lane group G at step kk is
+//      4 G + kk, so a C-layout result is directly the B operand of the next product.  A and T share one fp32 matrix M: A_ij = M[i][j] below the diagonal, T is
 //      stored transposed, T_ij = M[j][i] on and above it (T's upper triangle is zero).
 //   3  w^T = k^T T'^T and u^T = v^T T''^T with bf16 MFMA: the A operands are transposed reads of
 //      the k / v tiles, the B operands rows of T scaled per column and rounded to bf16; each lane
@@ -176,15 +176,15 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
     }
   }
   wait_lgkm0();
-  block_barrier();
 
   // T_rc (r >= c) lives at M[c][r]; entries above T's diagonal read as zero
   auto tval = [&](int r, int c) { return r >= c ? M[c * MS + r] : 0.f; };
 
-  // ---- phase 2a: diagonal blocks T_bb = (I + A_bb)^{-1}, lane = (block bb, column c).
-  // acc[r] collects 1_{r=c} - sum_{j<r} A_rj T_jc in the order j = 0, 1, ..., r-1.
-  if (wave == 0) {
-    const int bb = lane >> 4, c = lane & 15, o = 16 * bb;
+  // ---- phase 2a: this wave's diagonal block T_ww = (I + A_ww)^{-1}, right after it wrote
+  // A_ww (its own LDS writes are visible to its later reads without a barrier).  Lane c < 16
+  // solves column c; acc[r] collects 1_{r=c} - sum_{j<r} A_rj T_jc in the order j = 0, ..., r-1.
+  if (G == 0) {
+    const int c = n, o = 16 * wave;
     float acc[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = r == c ? 1.f : 0.f;
@@ -200,7 +200,10 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   wait_lgkm0();
   block_barrier();
 
-  // ---- phase 2b: off-diagonal blocks, one level per block distance
+  // ---- phase 2b: off-diagonal blocks by column block: wave j computes T_ij for i = j+1 .. 3 in
+  // order, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj.  Every A block and diagonal T block is in LDS
+  // after the barrier above, and the T_kj (k > j) it needs are its own earlier results, so no
+  // further barrier is needed.
   // acc += A[xr.., xc..] T[yr.., yc..] (16x16 blocks; A below the diagonal, T diagonal or below)
   auto mm = [&](f32x4 acc, int xr, int xc, int yr, int yc) {
 #pragma unroll
@@ -217,23 +220,14 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
     for (int r = 0; r < 4; ++r) M[(tc + n) * MS + tr + 4 * G + r] = -acc[r];
   };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-  if (wave >= 1) {   // distance 1: T_{w,w-1} = -T_ww A_{w,w-1} T_{w-1,w-1}
-    const int bi = 16 * wave, bj = 16 * (wave - 1);
-    finish(mm(z4, bi, bj, bj, bj), bi, bj);
-  }
-  wait_lgkm0();
-  block_barrier();
-  if (wave >= 2) {   // distance 2: T_{w,w-2} = -T_ww (A_{w,w-2} T_{w-2,w-2} + A_{w,w-1} T_{w-1,w-2})
-    const int bi = 16 * wave, bj = 16 * (wave - 2), bk = 16 * (wave - 1);
-    finish(mm(mm(z4, bi, bj, bj, bj), bi, bk, bk, bj), bi, bj);
-  }
-  wait_lgkm0();
-  block_barrier();
-  if (wave == 3) {   // distance 3: T_30 = -T_33 (A_30 T_00 + A_31 T_10 + A_32 T_20)
-    f32x4 x = mm(z4, 48, 0, 0, 0);
-    x = mm(x, 48, 16, 16, 0);
-    x = mm(x, 48, 32, 32, 0);
-    finish(x, 48, 0);
+#pragma unroll
+  for (int ib = 1; ib < 4; ++ib) {
+    if (ib <= wave) continue;
+    f32x4 y = z4;
+#pragma unroll
+    for (int kb = 0; kb < 3; ++kb)
+      if (kb >= wave && kb < ib) y = mm(y, 16 * ib, 16 * kb, 16 * kb, 16 * wave);
+    finish(y, 16 * ib, 16 * wave);
   }
   wait_lgkm0();
   block_barrier();
