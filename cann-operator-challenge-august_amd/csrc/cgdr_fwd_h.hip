@@ -170,14 +170,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
   }
   if (V % (16 * ncw) != 0) ncw = 1;
-  if (a->numerics == CGDR_NUMERICS_CONTEST) {
-    pl->kernel = 2;
-    pl->ncw = ncw;
-    pl->nlw = 0;
-    pl->stages = 1;
-    pl->threads = 64 * ncw;
-    pl->lds = 0;
-  } else if (a->in_dtype == CGDR_F32) {
+  if (a->in_dtype == CGDR_F32) {
     pl->kernel = 1;
     pl->ncw = ncw;
     pl->nlw = 0;
@@ -185,14 +178,16 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     pl->threads = 64 * ncw;
     pl->lds = 0;
   } else {
-    pl->kernel = 0;
-    pl->ncw = ncw;
+    // bf16: the pipelined kernel, with the contest rounding model when asked for
+    pl->kernel = a->numerics == CGDR_NUMERICS_CONTEST ? 2 : 0;
     if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
     int nlw = env_int("CGDR_FWD_H_LOADERS", 0);
     // With helper workgroups the task's loads are L2 hits and one load wave keeps up; at most
     // 8 waves per workgroup (two per SIMD), so that no wave is squeezed below 256 VGPRs.
-    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = use_helpers ? 1 : 2;
+    // K = 256: one load wave (two push the kernel past 256 VGPRs into scratch spills).
+    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = (use_helpers || K == 256) ? 1 : 2;
+    if (pl->kernel == 2 && nlw == 4) nlw = 2;   // contest instantiations: 1 or 2 load waves
     while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
     pl->nlw = nlw;
     int stages = env_int("CGDR_FWD_H_STAGES", 0);
@@ -208,7 +203,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   // Helper workgroups (one per task, on the task's XCD) when the doubled grid still fits the
   // chip at one workgroup per CU, so that tasks and helpers are all resident together.
   pl->helpers = 0;
-  if (pl->kernel == 0 && pl->tasks % 8 == 0 && 2 * pl->tasks <= kCUs && helpers_env != 0 &&
+  if (pl->kernel != 1 && pl->tasks % 8 == 0 && 2 * pl->tasks <= kCUs && helpers_env != 0 &&
       (use_helpers || helpers_env == 1))
     pl->helpers = 1;
   return CGDR_OK;
@@ -247,47 +242,47 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   return p;
 }
 
-template <int KD, int NCW, int NLW, int STAGES>
+template <int KD, int NCW, int NLW, int STAGES, bool CONTEST>
 hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
   using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
   const unsigned grid = (unsigned)(p.helpers ? 2 * tasks : tasks);
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES>), dim3(grid),
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, CONTEST>), dim3(grid),
                      dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 
-template <int KD, int NCW, bool CONTEST>
+template <int KD, int NCW>
 hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
   using L = cgdr::F32Layout<KD, NCW>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW, CONTEST>), dim3((unsigned)tasks), dim3(L::THREADS), 0,
-                     stream, p);
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
 
-template <int KD, int NCW, int NLW>
+template <int KD, int NCW, int NLW, bool CONTEST>
 hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4>())
-    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4>(p, pl.tasks, s);
+    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, CONTEST>(p, pl.tasks, s);
   if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3>())
-    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3>(p, pl.tasks, s);
-  return launch_bf16<KD, NCW, NLW, 2>(p, pl.tasks, s);
+    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, CONTEST>(p, pl.tasks, s);
+  return launch_bf16<KD, NCW, NLW, 2, CONTEST>(p, pl.tasks, s);
 }
 
-template <int KD, int NCW>
+template <int KD, int NCW, bool CONTEST>
 hipError_t dispatch_bf16_nlw(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1>(p, pl, s);
-  if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4>(p, pl, s);
-  return dispatch_bf16_stages<KD, NCW, 2>(p, pl, s);
+  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, CONTEST>(p, pl, s);
+  if constexpr (!CONTEST)
+    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, CONTEST>(p, pl, s);
+  return dispatch_bf16_stages<KD, NCW, 2, CONTEST>(p, pl, s);
 }
 
-template <int KD>
+template <int KD, bool CONTEST>
 hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (KD == 256) {
-    return dispatch_bf16_nlw<KD, 1>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, CONTEST>(p, pl, s);
   } else {
-    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2>(p, pl, s);
-    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4>(p, pl, s);
-    return dispatch_bf16_nlw<KD, 1>(p, pl, s);
+    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, CONTEST>(p, pl, s);
+    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, CONTEST>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, CONTEST>(p, pl, s);
   }
 }
 
@@ -332,15 +327,15 @@ int bf16_max_stages(int64_t K, int ncw, int nlw) {
   }
 }
 
-template <int KD, bool CONTEST>
+template <int KD>
 hipError_t dispatch_f32(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.ncw == 2) return launch_f32<KD, 2, CONTEST>(p, pl.tasks, s);
-  if (pl.ncw == 4) return launch_f32<KD, 4, CONTEST>(p, pl.tasks, s);
-  return launch_f32<KD, 1, CONTEST>(p, pl.tasks, s);
+  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
+  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
+  return launch_f32<KD, 1>(p, pl.tasks, s);
 }
 
 int lds_bytes_of(const Plan& pl, int64_t K) {
-  if (pl.kernel == 1 || pl.kernel == 2) {
+  if (pl.kernel == 1) {
     auto f32 = [&](auto kd) -> int {
       constexpr int KD = decltype(kd)::value;
       return pl.ncw == 1 ? cgdr::F32Layout<KD, 1>::LDS_BYTES
@@ -457,23 +452,23 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
   }
   if (pl.kernel == 0) {
     switch (args->K) {
-      case 32: e = dispatch_bf16<32>(p, pl, s); break;
-      case 64: e = dispatch_bf16<64>(p, pl, s); break;
-      case 128: e = dispatch_bf16<128>(p, pl, s); break;
-      default: e = dispatch_bf16<256>(p, pl, s); break;
+      case 32: e = dispatch_bf16<32, false>(p, pl, s); break;
+      case 64: e = dispatch_bf16<64, false>(p, pl, s); break;
+      case 128: e = dispatch_bf16<128, false>(p, pl, s); break;
+      default: e = dispatch_bf16<256, false>(p, pl, s); break;
     }
   } else if (pl.kernel == 1) {
     switch (args->K) {
-      case 32: e = dispatch_f32<32, false>(p, pl, s); break;
-      case 64: e = dispatch_f32<64, false>(p, pl, s); break;
-      default: e = dispatch_f32<128, false>(p, pl, s); break;
+      case 32: e = dispatch_f32<32>(p, pl, s); break;
+      case 64: e = dispatch_f32<64>(p, pl, s); break;
+      default: e = dispatch_f32<128>(p, pl, s); break;
     }
   } else {
     switch (args->K) {
-      case 32: e = dispatch_f32<32, true>(p, pl, s); break;
-      case 64: e = dispatch_f32<64, true>(p, pl, s); break;
-      case 128: e = dispatch_f32<128, true>(p, pl, s); break;
-      default: e = dispatch_f32<256, true>(p, pl, s); break;
+      case 32: e = dispatch_bf16<32, true>(p, pl, s); break;
+      case 64: e = dispatch_bf16<64, true>(p, pl, s); break;
+      case 128: e = dispatch_bf16<128, true>(p, pl, s); break;
+      default: e = dispatch_bf16<256, true>(p, pl, s); break;
     }
   }
   if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));

@@ -35,6 +35,17 @@
 // beside the compute waves).
 // One s_barrier per chunk hands stages over; no wave waits on another wave's memory
 // counters, and no wave mixes VMEM loads and stores (which would force vmcnt(0)).
+//
+// CONTEST = true runs the numerics of the contest reference run() (docs/problem.txt:81-167;
+// code/tests/golden/generate_golden.py:350-440), "O2", on the same pipeline:
+//   state S in bf16;  ws = bf16(W S);  v16 = f16sat(f16sat(u) - nan_to_num(fp16(ws)))
+//   v_new = bf16(v16);  vd = bf16(f16sat(v16 * f16sat(exp(g_last - g))))
+//   hd = f16sat(f16sat(S) * fp16(exp(fp16(g_last))));  up = nan_to_num(fp16(bf16(K^T vd)))
+//   S = bf16(bf16(hd) + bf16(up))
+// where f16sat is the reference's cast_to_float16 (round to fp16, finite overflow saturates to
+// +-65504, inf and NaN pass through).  The operands are bf16, so the MFMA products are the bf16
+// GEMMs' products, accumulated in fp32 and rounded once to bf16: MM1 starts from zero instead of
+// U, and MM2 accumulates K^T vd alone, combined with the decayed state after it.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -149,6 +160,19 @@ __device__ __forceinline__ float bf16_lo(unsigned x) { return __uint_as_float(x 
 __device__ __forceinline__ float bf16_hi(unsigned x) { return __uint_as_float(x & 0xffff0000u); }
 
 __device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? expf(x) : 0.f; }
+
+// cast_to_float16 (code/tests/golden/generate_golden.py:285-290), returned as its fp32 value
+__device__ __forceinline__ float f16_sat(float x) {
+  float r = (float)(_Float16)x;
+  if (__builtin_isfinite(x)) r = fminf(fmaxf(r, -65504.f), 65504.f);
+  return r;
+}
+// torch.nan_to_num(x.to(float16), nan=0, posinf=inf, neginf=-inf)
+__device__ __forceinline__ float f16_nan_to_num(float x) {
+  const float r = (float)(_Float16)x;
+  return r != r ? 0.f : r;
+}
+__device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
 
 // ---------------------------------------------------------------------------------------------
 // Swizzles of 16-byte pieces inside LDS tiles (P = pieces per row).  Each is chosen so that the
@@ -296,7 +320,7 @@ constexpr int bf16_max_stages() {
   return bf16_config_ok<KD, NCW, NLW, 4>() ? 4 : bf16_config_ok<KD, NCW, NLW, 3>() ? 3 : 2;
 }
 
-template <int KD, int NCW, int NLW, int STAGES>
+template <int KD, int NCW, int NLW, int STAGES, bool CONTEST = false>
 __global__ void __launch_bounds__(64 * (NCW + NLW + NCW + 1))
 cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   using L = Bf16Layout<KD, NCW, NLW, STAGES>;
@@ -336,8 +360,14 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     float gamma, a;
     if (has_g) {
       const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
-      gamma = lane < len ? safe_exp(glast - gv) : 0.f;
-      a = expf(glast);
+      if constexpr (CONTEST) {
+        // fp16 gate of every token and fp16 exp of the fp16 g_last (generate_golden.py:409-416)
+        gamma = lane < len ? f16_sat(expf(glast - gv)) : 0.f;
+        a = (float)(_Float16)expf(f16_sat(glast));
+      } else {
+        gamma = lane < len ? safe_exp(glast - gv) : 0.f;
+        a = expf(glast);
+      }
     } else {
       gamma = lane < len ? 1.f : 0.f;
       a = 1.f;
@@ -464,6 +494,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           const int64_t off = base + (int64_t)krow * p.V + vcol;
           S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off]
                               : bf16_lo(((const unsigned short*)p.h0)[off]);
+          if constexpr (CONTEST) S[kt][r] = bf16_rnd(S[kt][r]);   // the state is bf16
         }
     } else {
 #pragma unroll
@@ -528,7 +559,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       f32x4 acc[4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
-        acc[tt] = f32x4{bf16_lo(uraw[tt][0]), bf16_hi(uraw[tt][0]), bf16_lo(uraw[tt][1]), bf16_hi(uraw[tt][1])};
+        acc[tt] = CONTEST ? f32x4{0.f, 0.f, 0.f, 0.f}   // W S is its own bf16 GEMM
+                          : f32x4{bf16_lo(uraw[tt][0]), bf16_hi(uraw[tt][0]), bf16_lo(uraw[tt][1]), bf16_hi(uraw[tt][1])};
       __builtin_amdgcn_sched_barrier(0);
 
       // Phase 2: MM1 acc[tt] = U_tt + W_tt bf16(-S), four independent chains issued k-block
@@ -551,13 +583,24 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       };
       u32x4 kop0[KT], kop1[KT];
+      unsigned hdp[CONTEST ? KT : 1][2];   // contest: bf16(hd) pairs of the decayed state
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
           acc[tt] = mfma_bf16(__builtin_bit_cast(bf16x8, wop[tt][kb]), __builtin_bit_cast(bf16x8, Sw[kb]), acc[tt]);
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) S[kt] = S[kt] * a;
+      for (int kt = 0; kt < KT; ++kt) {
+        if constexpr (CONTEST) {
+          // hd = f16sat(f16sat(S) a) kept as bf16(hd); S becomes the K^T Vd accumulator
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+            hdp[kt][r] = pack_bf16x2(f16_sat(f16_sat(S[kt][2 * r]) * a), f16_sat(f16_sat(S[kt][2 * r + 1]) * a));
+          S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+          S[kt] = S[kt] * a;
+        }
+      }
       read_kop(0, kop0);
 #pragma unroll
       for (int i = 0; i < 4 * KB; ++i) {
@@ -576,8 +619,19 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         for (int j = 0; j < 4; ++j) {
           const int hh = j >> 1, r = 2 * (j & 1);
           const float v0 = acc[2 * tb + hh][r], v1 = acc[2 * tb + hh][r + 1];
-          pv[j] = pack_bf16x2(v0, v1);
-          pd[j] = pack_bf16x2(v0 * gm[tb][hh][r], v1 * gm[tb][hh][r + 1]);
+          if constexpr (CONTEST) {
+            // acc = -W S: ws = nan_to_num(fp16(bf16(W S))), v16 = f16sat(f16sat(u) - ws)
+            const u32x2 ur = uraw[2 * tb + hh];
+            const float u0 = r == 0 ? bf16_lo(ur[0]) : bf16_lo(ur[1]);
+            const float u1 = r == 0 ? bf16_hi(ur[0]) : bf16_hi(ur[1]);
+            const float x0 = f16_sat(f16_sat(u0) - f16_nan_to_num(-bf16_rnd(v0)));
+            const float x1 = f16_sat(f16_sat(u1) - f16_nan_to_num(-bf16_rnd(v1)));
+            pv[j] = pack_bf16x2(x0, x1);
+            pd[j] = pack_bf16x2(f16_sat(x0 * gm[tb][hh][r]), f16_sat(x1 * gm[tb][hh][r + 1]));
+          } else {
+            pv[j] = pack_bf16x2(v0, v1);
+            pd[j] = pack_bf16x2(v0 * gm[tb][hh][r], v1 * gm[tb][hh][r + 1]);
+          }
         }
         sv[vrow * 8 + ((4 * tb + g) ^ swz_v(vrow))] = pv;
         return __builtin_bit_cast(bf16x8, pd);
@@ -601,6 +655,17 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       // Phase 5: MM2 of token block 1.
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[kt]), Vd1, S[kt]);
+      if constexpr (CONTEST) {
+        // S = bf16(bf16(hd) + bf16(nan_to_num(fp16(bf16(K^T Vd)))))
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const unsigned hw = hdp[kt][r >> 1];
+            const float hd = (r & 1) ? bf16_hi(hw) : bf16_lo(hw);
+            S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[kt][r]))));
+          }
+      }
       wait_lgkm0();
       block_barrier();   // B_c
     };
@@ -897,30 +962,8 @@ static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __re
 // (pi, sigma) with v_mfma_f32_16x16x4_f32, whose operands are one element per lane, so no
 // transposed reads are needed.  All waves load the next chunk with plain loads; it is the
 // exact-arithmetic path (fp32 products, fp32 accumulation) and is not the performance path.
-//
-// CONTEST = true is the same kernel for bf16 k/w/u with the numerics of the contest reference
-// run() (docs/problem.txt:81-167; code/tests/golden/generate_golden.py:350-440), "O2":
-//   state S in bf16;  ws = bf16(W S);  v16 = f16sat(f16sat(u) - nan_to_num(fp16(ws)))
-//   v_new = bf16(v16);  vd = bf16(f16sat(v16 * f16sat(exp(g_last - g))))
-//   hd = f16sat(f16sat(S) * fp16(exp(fp16(g_last))));  up = nan_to_num(fp16(bf16(K^T vd)))
-//   S = bf16(bf16(hd) + bf16(up))
-// where f16sat is the reference's cast_to_float16 (round to fp16, finite overflow saturates to
-// +-65504, inf and NaN pass through).  bf16 values are exact in fp32, so the fp32 MFMA products
-// are the bf16 GEMM's products, accumulated in fp32 and rounded once to bf16.
 // =============================================================================================
 
-// cast_to_float16 (code/tests/golden/generate_golden.py:285-290), returned as its fp32 value
-__device__ __forceinline__ float f16_sat(float x) {
-  float r = (float)(_Float16)x;
-  if (__builtin_isfinite(x)) r = fminf(fmaxf(r, -65504.f), 65504.f);
-  return r;
-}
-// torch.nan_to_num(x.to(float16), nan=0, posinf=inf, neginf=-inf)
-__device__ __forceinline__ float f16_nan_to_num(float x) {
-  const float r = (float)(_Float16)x;
-  return r != r ? 0.f : r;
-}
-__device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
 template <int KD, int NCW>
 struct F32Layout {
   static constexpr int VT = 16 * NCW;
@@ -933,7 +976,7 @@ struct F32Layout {
   static constexpr int THREADS = 64 * NCW;
 };
 
-template <int KD, int NCW, bool CONTEST = false>
+template <int KD, int NCW>
 __global__ void __launch_bounds__(64 * NCW)
 cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   using L = F32Layout<KD, NCW>;
@@ -954,8 +997,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   const int g = lane >> 4, n = lane & 15;
   const int vcol = vbase + 16 * wave + n;
 
-  // element type of k/w/u/h/v_new: fp32, or bf16 in contest mode
-  using E = std::conditional_t<CONTEST, __bf16, float>;
+  using E = float;   // element type of k/w/u/h/v_new
   const E* kb_ = (const E*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
   const E* wb_ = (const E*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
   const E* ub_ = (const E*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
@@ -973,7 +1015,6 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (int64_t)krow * p.V + vcol;
         S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
-        if constexpr (CONTEST) S[kt][r] = bf16_rnd(S[kt][r]);   // the state is bf16
       }
   } else {
 #pragma unroll
@@ -984,25 +1025,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     const int64_t t0 = tk.bos + (int64_t)c * kChunk;
     const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
     __syncthreads();
-    if constexpr (CONTEST) {
-      // bf16 rows are 16-byte aligned (checked on the host): 8 elements per load
-      auto widen = [](const u32x4& x, float* dst) {
-        const f32x4 lo = {bf16_lo(x[0]), bf16_hi(x[0]), bf16_lo(x[1]), bf16_hi(x[1])};
-        const f32x4 hi = {bf16_lo(x[2]), bf16_hi(x[2]), bf16_lo(x[3]), bf16_hi(x[3])};
-        *(f32x4*)dst = lo;
-        *(f32x4*)(dst + 4) = hi;
-      };
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      for (int idx = threadIdx.x; idx < 64 * KD / 8; idx += L::THREADS) {
-        const int r = idx / (KD / 8), col = 8 * (idx % (KD / 8));
-        widen(r < len ? *(const u32x4*)(wb_ + (t0 + r) * p.sw_t + col) : z, Ws + r * WP + col);
-        widen(r < len ? *(const u32x4*)(kb_ + (t0 + r) * p.sk_t + col) : z, Ks + r * WP + col);
-      }
-      for (int idx = threadIdx.x; idx < 64 * VT / 8; idx += L::THREADS) {
-        const int r = idx / (VT / 8), col = 8 * (idx % (VT / 8));
-        widen(r < len ? *(const u32x4*)(ub_ + (t0 + r) * p.su_t + col) : z, Us + r * UP + col);
-      }
-    } else {
+    {
       for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
         const int r = idx / KD, col = idx % KD;
         Ws[r * WP + col] = r < len ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
@@ -1019,23 +1042,15 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       float gamma = t < len ? 1.f : 0.f, a = 1.f;
       if (gb_ != nullptr) {
         const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
-        if constexpr (CONTEST) {
-          // fp16 gate of every token and fp16 exp of the fp16 g_last (generate_golden.py:409-416)
-          gamma = t < len ? f16_sat(expf(glast - gv)) : 0.f;
-          a = (float)(_Float16)expf(f16_sat(glast));
-        } else {
-          gamma = t < len ? safe_exp(glast - gv) : 0.f;
-          a = expf(glast);
-        }
-      } else if constexpr (CONTEST) {
-        a = 1.f;   // exp(0) in every precision
+        gamma = t < len ? safe_exp(glast - gv) : 0.f;
+        a = expf(glast);
       }
       Gs[t] = gamma;
       if (t == 0) Gs[64] = a;
     }
     __syncthreads();
 
-    // h snapshot (exact: fp32, or the bf16 state in contest mode)
+    // h snapshot (exact)
     {
       E* hdst = hb_ + (tk.boh + c) * p.sh_c;
 #pragma unroll
@@ -1068,24 +1083,14 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-        if constexpr (CONTEST) {
-          const float ws = f16_nan_to_num(bf16_rnd(acc[tt][r]));
-          const float v16 = f16_sat(f16_sat(Us[t * UP + 16 * wave + n]) - ws);
-          if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = (E)v16;
-          Vd[tt][r] = t < len ? bf16_rnd(f16_sat(v16 * Gs[t])) : 0.f;
-        } else {
-          const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
-          if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
-          Vd[tt][r] = vn * Gs[t];
-        }
+        const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
+        if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+        Vd[tt][r] = vn * Gs[t];
       }
-    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r));
-    // contest mode: the update is its own bf16 GEMM, combined with the decayed state in bf16
+    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r))
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt) {
-      f32x4 up;
-      if constexpr (CONTEST) up = f32x4{0.f, 0.f, 0.f, 0.f};
-      else up = S[kt] * a;
+      f32x4 up = S[kt] * a;
       const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
@@ -1094,15 +1099,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
           const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
           up = mfma_f32(Ks[t * WP + krow], Vd[tt][r], up);
         }
-      if constexpr (CONTEST) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float hd = f16_sat(f16_sat(S[kt][r]) * a);
-          S[kt][r] = bf16_rnd(bf16_rnd(hd) + bf16_rnd(f16_nan_to_num(bf16_rnd(up[r]))));
-        }
-      } else {
-        S[kt] = up;
-      }
+      S[kt] = up;
     }
   }
   if (p.final_state != nullptr) {

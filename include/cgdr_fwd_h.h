@@ -70,8 +70,8 @@ typedef enum cgdr_dtype {
  *     fp32 state, bf16(S) and bf16(gated v_new) as GEMM operands; fp32 inputs are exact fp32.
  *   CGDR_NUMERICS_CONTEST: bf16 inputs only; the contest reference run() /
  *     run_reference (docs/problem.txt:81-167, code/tests/golden/generate_golden.py:350-440):
- *     bf16 state, bf16 GEMM outputs, saturating fp16 casts and nan_to_num after each GEMM.
- *     A simpler, slower kernel (not the pipelined one). */
+ *     bf16 state, bf16 GEMM outputs, saturating fp16 casts and nan_to_num after each GEMM,
+ *     on the same pipelined kernel. */
 typedef enum cgdr_numerics {
   CGDR_NUMERICS_DEFAULT = 0,
   CGDR_NUMERICS_CONTEST = 1
