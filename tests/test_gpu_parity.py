@@ -90,6 +90,32 @@ def test_config4_wide_value_strong_decay(dev):
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
+def test_config3_varlen_full_size(dev):
+    """Config 3 at its full size: 16 sequences of seeded lengths in [64, 8192] (none a multiple
+    of 64), H=32, K=V=128, per-sequence h0, BASELINE's distributions.  All heads against the
+    bf16 rounding model elementwise (rtol=2e-2, atol=2e-3); every fourth head against the exact
+    recurrence within 1% of the tensor's scale."""
+    cu = O.varlen_cu_seqlens(3, 16, 64, 8192)
+    inp = _case(31, 1, int(cu[-1]), 32, 128, 128, cu=cu)
+    out = [np32(x) for x in abi_call(dev_inputs(inp, torch.bfloat16, dev))]
+    for name, got, r1 in zip(("h", "v_new", "final"), out, O.fwd_h(**inp, rounding="bf16")):
+        assert_close(got, r1, name=f"{name} vs bf16 model", **BF16_TOL)
+    heads = slice(0, 32, 4)
+    sub = dict(inp, k=inp["k"][:, :, heads], w=inp["w"][:, :, heads], u=inp["u"][:, :, heads],
+               g=inp["g"][:, :, heads], initial_state=inp["initial_state"][:, heads])
+    ref3 = O.fwd_h(**sub)
+    for name, got, r3, ax in zip(("h", "v_new", "final"), out, ref3, (2, 2, 1)):
+        got = np.take(got, np.arange(32)[heads], axis=ax)
+        assert_scale_close(got, r3, 1e-2, name=f"{name} vs exact")
+
+
+def test_config4_full_size(dev):
+    """Config 4 at its full size: B=4, T=8192, H=8, K=128, V=256, g the chunk-local cumsum of
+    logsigmoid(randn - 2), so exp(g) spans ~1e-30 .. 1."""
+    inp = _case(41, 4, 8192, 8, 128, 256, shift=-2.0)
+    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
+
+
 # ---------------------------------------------------------------- shapes and edge cases
 
 @pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (64, 128), (128, 64), (256, 256), (256, 64)])
