@@ -12,8 +12,9 @@
 // reference, and its device stage 1, op_kernel/arch22/chunk_gated_delta_rule_stage1.h.)
 //
 // Phases, separated by workgroup barriers:
-//   0  DMA of the k and v tiles into LDS; wave 0 forms g (each lane sums a_0..a_i in order,
-//      which is the sequential cumsum bit for bit), beta e^g and beta
+//   0  DMA of the k tile into LDS; wave 0 forms g (each lane sums a_0..a_i in order, which is
+//      the sequential cumsum bit for bit), beta e^g and beta.  Then each wave touches its share
+//      of this unit's v rows and of a later unit's k rows into L2.
 //   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, operands read from the k tile),
 //      A written to LDS in fp32
 //   2  T: each wave inverts its own 16x16 diagonal block by forward substitution right after
@@ -21,11 +22,14 @@
 //      later rows at once, so the dependent chain is 16 steps); after one barrier, wave j computes
 //      column block j, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj for i = j+1 .. 3 in order, with fp32
 //      MFMA 16x16x4 and no further barrier.  The contraction slot of lane group G at step kk is
-//      4 G + kk, so a C-layout result is directly the B operand of the next product.  A and T share one fp32 matrix M: A_ij = M[i][j] below the diagonal, T is
-//      stored transposed, T_ij = M[j][i] on and above it (T's upper triangle is zero).
+//      4 G + kk, so a C-layout result is directly the B operand of the next product.  A and T
+//      share one fp32 matrix M: A_ij = M[i][j] below the diagonal, T is stored transposed,
+//      T_ij = M[j][i] on and above it (T's upper triangle is zero).
 //   3  w^T = k^T T'^T and u^T = v^T T''^T with bf16 MFMA: the A operands are transposed reads of
 //      the k / v tiles, the B operands rows of T scaled per column and rounded to bf16; each lane
-//      ends with 8 consecutive columns of one token, written with 16-byte stores.
+//      ends with 8 consecutive columns of one token, written with 16-byte stores.  The B operands
+//      go to registers first; the v tile then takes M's place in LDS (its DMA runs while w is
+//      computed), so a workgroup needs k, M and g only: 34,816 B at K = V = 128.
 #pragma once
 
 #include "cgdr_chunk_common.h"
@@ -51,6 +55,7 @@ struct WyParams {
   int64_t sw_b, sw_t, sw_h;
   int64_t su_b, su_t, su_h;
   int64_t sc_b, sc_t, sc_h;
+  int32_t pf_lead;   // L2 prefetch: workgroups ahead (a multiple of 8), 0 = off
 };
 
 template <int KD, int VD>
@@ -58,9 +63,10 @@ struct WyLayout {
   static constexpr int PK = KD / 8, PV = VD / 8;   // 16-byte pieces per k / v tile row
   static constexpr int MS = 68;                    // fp32 row stride of A and T (conflict-free columns)
   static constexpr int K_OFF = 0;                  // k tile [64][KD] bf16
-  static constexpr int V_OFF = 64 * KD * 2;        // v tile [64][VD] bf16
-  static constexpr int M_OFF = V_OFF + 64 * VD * 2;   // A (strictly lower) and T^T (upper), fp32
-  static constexpr int G_OFF = M_OFF + 64 * MS * 4;   // g [64], beta e^g [64], beta [64], a [64]
+  static constexpr int M_OFF = 64 * KD * 2;        // A (strictly lower) and T^T (upper), fp32
+  static constexpr int V_OFF = M_OFF;              // v tile [64][VD] bf16, once T is in registers
+  static constexpr int MV_BYTES = 64 * MS * 4 > 64 * VD * 2 ? 64 * MS * 4 : 64 * VD * 2;
+  static constexpr int G_OFF = M_OFF + MV_BYTES;   // g [64], beta e^g [64], beta [64], a [64]
   static constexpr int LDS_BYTES = G_OFF + 4 * 256;
   static constexpr int RPDK = 64 / PK, RPDV = 64 / PV;
   static constexpr int DMA_K = 64 / RPDK, DMA_V = 64 / RPDV;
@@ -95,10 +101,10 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   __bf16* wb = (__bf16*)p.w + b * p.sw_b + start * p.sw_t + head * p.sw_h;
   __bf16* ub = (__bf16*)p.u + b * p.su_b + start * p.su_t + head * p.su_h;
 
-  // ---- phase 0: k and v tiles (rows past the chunk end zero-filled)
+  // ---- phase 0: k tile (rows past the chunk end zero-filled); the v tile follows in phase 3
   const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
   {
-    const int64_t krow = p.sk_t * 2, vrow = p.sv_t * 2;
+    const int64_t krow = p.sk_t * 2;
 #pragma unroll
     for (int m = 0; m < L::DMA_K; ++m) {
       if (m % 4 != wave) continue;
@@ -107,15 +113,6 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
         dma_b128(kb, (uint32_t)(r * krow) + 16u * (uint32_t)(c ^ swz_k<L::PK>(r)), lds0 + L::K_OFF + 1024u * m);
       else
         *(u32x4*)(smem + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int m = 0; m < L::DMA_V; ++m) {
-      if ((L::DMA_K + m) % 4 != wave) continue;
-      const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
-      if (r < len)
-        dma_b128(vb, (uint32_t)(r * vrow) + 16u * (uint32_t)(c ^ swz_k<L::PV>(r)), lds0 + L::V_OFF + 1024u * m);
-      else
-        *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
     }
   }
   float* GA = (float*)(smem + L::G_OFF);
@@ -145,6 +142,38 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   wait_vm<0>();
   wait_lgkm0();
   block_barrier();
+
+  // ---- L2 prefetch: the v rows of this unit (loaded into LDS in phase 3) and the k rows of the
+  // unit of workgroup blockIdx + pf_lead.  Workgroups are dealt to the 8 XCDs round-robin, so
+  // with pf_lead a multiple of 8 that unit runs on this XCD, about pf_lead / (resident
+  // workgroups) unit lifetimes from now, and finds its rows in this XCD's L2.  One 4-byte
+  // direct-to-LDS load per 128-byte line, landing in the a[] slot of the g area (not read after
+  // phase 0); each wave drains its own before the barrier ahead of phase 3.
+  {
+    constexpr int LK = KD >= 64 ? KD / 64 : 1, LV = VD >= 64 ? VD / 64 : 1;   // lines per row
+    const uint32_t trash = lds0 + L::G_OFF + 768u;
+#pragma unroll
+    for (int m = 0; m < LV; ++m) {
+      if ((LK + m) % 4 != wave) continue;
+      const int t = 64 * m + lane, r = t / LV;
+      if (r < len) dma_b32_addr((const char*)vb + r * p.sv_t * 2 + 128 * (t % LV), trash);
+    }
+    if (p.pf_lead > 0 && (int64_t)blockIdx.x + p.pf_lead < (int64_t)gridDim.x) {
+      int64_t u2 = xcd_remap(blockIdx.x + p.pf_lead, gridDim.x);
+      const int head2 = (int)(u2 % p.H);
+      u2 /= p.H;
+      const ChunkRange cr2 = chunk_range(p.T, p.N, p.cu_seqlens, p.chunk_indices, u2 % p.NT);
+      const int b2 = (int)(u2 / p.NT);
+      const int len2 = __builtin_amdgcn_readfirstlane(cr2.len);
+      const char* k2 = (const char*)p.k + 2 * (b2 * p.sk_b + cr2.start * p.sk_t + (head2 / (p.H / p.Hg)) * p.sk_h);
+#pragma unroll
+      for (int m = 0; m < LK; ++m) {
+        if (m % 4 != wave) continue;
+        const int t = 64 * m + lane, r = t / LK;
+        if (r < len2) dma_b32_addr(k2 + r * p.sk_t * 2 + 128 * (t % LK), trash);
+      }
+    }
+  }
 
   // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i); lane holds S[16t + 4G + r][i].
   // Operands are k rows from the tile: row j, contraction slice 32 ks + 8 G .. +7 (one piece).
@@ -230,49 +259,79 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
     finish(y, 16 * ib, 16 * wave);
   }
   wait_lgkm0();
+  wait_vm<0>();   // the prefetch loads (issued two phases ago) have landed
   block_barrier();
-  if (16 * wave >= len) return;
 
-  // ---- phase 3: w^T = k^T T'^T, u^T = v^T T''^T for this wave's tokens i
-  const int njp = (wave >> 1) + 1;   // contraction j <= i < 16 wave + 16
+  // ---- phase 3: w^T = k^T T'^T, u^T = v^T T''^T for this wave's tokens i.  The B operands
+  // (rows of T scaled per column, bf16) go to registers first, so that the v tile can take the
+  // A/T matrix's place: its DMA (rows mostly in L2 by now) runs while w is computed.
+  const bool active = 16 * wave < len;   // wave-uniform; idle waves still share the DMA and barriers
+  const int njp = (wave >> 1) + 1;       // contraction j <= i < 16 wave + 16
   u32x4 bw[2], bu[2];
+  if (active) {
 #pragma unroll
-  for (int jp = 0; jp < 2; ++jp) {
-    if (jp >= njp) continue;
-    const int j0 = 32 * jp + 8 * G;
-    float tw[8], tu[8];
+    for (int jp = 0; jp < 2; ++jp) {
+      if (jp >= njp) continue;
+      const int j0 = 32 * jp + 8 * G;
+      float tw[8], tu[8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f32x4 sg = *(const f32x4*)(GA + 64 + j0 + 4 * h);
-      const f32x4 sb = *(const f32x4*)(GA + 128 + j0 + 4 * h);
+      for (int h = 0; h < 2; ++h) {
+        const f32x4 sg = *(const f32x4*)(GA + 64 + j0 + 4 * h);
+        const f32x4 sb = *(const f32x4*)(GA + 128 + j0 + 4 * h);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float t = tval(i, j0 + 4 * h + r);
-        tw[4 * h + r] = t * sg[r];
-        tu[4 * h + r] = t * sb[r];
+        for (int r = 0; r < 4; ++r) {
+          const float t = tval(i, j0 + 4 * h + r);
+          tw[4 * h + r] = t * sg[r];
+          tu[4 * h + r] = t * sb[r];
+        }
       }
+      bw[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
+      bu[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
     }
-    bw[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
-    bu[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
   }
+  wait_lgkm0();
+  block_barrier();   // every wave is done with A/T
+
+  {
+    const int64_t vrow = p.sv_t * 2;
+#pragma unroll
+    for (int m = 0; m < L::DMA_V; ++m) {
+      if ((L::DMA_K + m) % 4 != wave) continue;
+      const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
+      if (r < len)
+        dma_b128(vb, (uint32_t)(r * vrow) + 16u * (uint32_t)(c ^ swz_k<L::PV>(r)), lds0 + L::V_OFF + 1024u * m);
+      else
+        *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+    }
+  }
+  u32x4 wpk[KD / 32];   // w of token i, columns 32 pp + 8 G .. +7, held until the v tile lands
+  if (active) {
+#pragma unroll
+    for (int pp = 0; pp < KD / 32; ++pp) {
+      f32x4 acc[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp)
+          if (jp < njp)
+            acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PK>(ktile, 32 * jp, pp, x, G, e, qd)),
+                               __builtin_bit_cast(bf16x8, bw[jp]), acc[x]);
+      }
+      wpk[pp] = u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                      pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+    }
+  }
+  wait_vm<0>();
+  wait_lgkm0();
+  block_barrier();   // v tile in LDS
+  if (!active) return;
+
   const lds_char* vtile = (const lds_char*)smem + L::V_OFF;
   const bool store = i < len;
+  if (store) {
 #pragma unroll
-  for (int pp = 0; pp < KD / 32; ++pp) {
-    f32x4 acc[2];
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int jp = 0; jp < 2; ++jp)
-        if (jp < njp)
-          acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PK>(ktile, 32 * jp, pp, x, G, e, qd)),
-                             __builtin_bit_cast(bf16x8, bw[jp]), acc[x]);
-    }
-    if (store)
-      *(u32x4*)(wb + i * p.sw_t + 32 * pp + 8 * G) =
-          u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
-                pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+    for (int pp = 0; pp < KD / 32; ++pp) *(u32x4*)(wb + i * p.sw_t + 32 * pp + 8 * G) = wpk[pp];
   }
 #pragma unroll
   for (int pp = 0; pp < VD / 32; ++pp) {
