@@ -175,35 +175,38 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
     }
   }
 
-  // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i); lane holds S[16t + 4G + r][i].
-  // Operands are k rows from the tile: row j, contraction slice 32 ks + 8 G .. +7 (one piece).
+  // ---- phase 1: A_ij = beta_i S_ij e^{g_i - g_j} (j < i) by 16x16 tiles (row block rb, column
+  // block t <= rb); for tile (rb, t) lane holds S[16t + 4G + r][16rb + n].  Operands are k rows
+  // from the tile: row j, contraction slice 32 ks + 8 G .. +7 (one piece).  The ten tiles are
+  // dealt 3, 3, 2, 2: wave w computes its diagonal tile (w, w), then (2,0) (1,0) (2,1) (3,2)
+  // for w = 0..3, then (3,0) (3,1) for w = 0, 1.
   float* M = (float*)(smem + L::M_OFF);
   const int i = 16 * wave + n;
   const lds_char* ktile = (const lds_char*)smem + L::K_OFF;
   auto krow = [&](int j, int ks) {
     return __builtin_bit_cast(bf16x8, *(const u32x4*)(ktile + (j * L::PK + ((4 * ks + G) ^ swz_k<L::PK>(j))) * 16));
   };
-  {
-    const float gi = GA[i], bi = GA[128 + i];
+  auto a_tile = [&](int rb, int t) {
+    const int ii = 16 * rb + n;
+    const float gi = GA[ii], bi = GA[128 + ii];
     bf16x8 kc[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kc[ks] = krow(i, ks);
+    for (int ks = 0; ks < KS; ++ks) kc[ks] = krow(ii, ks);
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (t > wave) continue;
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < KS; ++ks) c = mfma_bf16(krow(16 * t + n, ks), kc[ks], c);
+    const f32x4 gj = *(const f32x4*)(GA + 16 * t + 4 * G);
+    f32x4 a;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) c = mfma_bf16(krow(16 * t + n, ks), kc[ks], c);
-      const f32x4 gj = *(const f32x4*)(GA + 16 * t + 4 * G);
-      f32x4 a;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * t + 4 * G + r;
-        a[r] = j < i ? bi * c[r] * expf(gi - gj[r]) : 0.f;
-      }
-      *(f32x4*)(M + i * MS + 16 * t + 4 * G) = a;
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * t + 4 * G + r;
+      a[r] = j < ii ? bi * c[r] * expf(gi - gj[r]) : 0.f;
     }
-  }
+    *(f32x4*)(M + ii * MS + 16 * t + 4 * G) = a;
+  };
+  a_tile(wave, wave);
+  a_tile(wave == 0 ? 2 : wave, wave == 0 ? 0 : wave - 1);
+  if (wave < 2) a_tile(3, wave);
   wait_lgkm0();
 
   // T_rc (r >= c) lives at M[c][r]; entries above T's diagonal read as zero
@@ -262,16 +265,26 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   wait_vm<0>();   // the prefetch loads (issued two phases ago) have landed
   block_barrier();
 
-  // ---- phase 3: w^T = k^T T'^T, u^T = v^T T''^T for this wave's tokens i.  The B operands
-  // (rows of T scaled per column, bf16) go to registers first, so that the v tile can take the
-  // A/T matrix's place: its DMA (rows mostly in L2 by now) runs while w is computed.
+  // ---- phase 3: w^T = k^T T'^T, u^T = v^T T''^T.  The B operands (rows of T scaled per column,
+  // bf16) go to registers first, so that the v tile can take the A/T matrix's place: its DMA
+  // (rows mostly in L2 by now) runs while w is computed.  The work comes in units of 32 output
+  // columns of [w | u] per token block, NPP units per block; a unit of token block tb costs
+  // 2 njp MFMAs (contraction j <= i: njp = 1 for blocks 0 and 1, 2 for blocks 2 and 3).  Wave w
+  // takes token block w; when Q = NPP / 4 units are all w columns, waves 2 and 3 leave units
+  // 0 .. Q-1 of their blocks to waves 0 and 1 (wave w takes them for block 3 - w), so every wave
+  // does 1.5 NPP units' worth of MFMAs.
+  constexpr int NPW = KD / 32, NPP = (KD + VD) / 32;
+  constexpr int Q = (NPP % 4 == 0 && NPP / 4 <= NPW) ? NPP / 4 : 0;
   const bool active = 16 * wave < len;   // wave-uniform; idle waves still share the DMA and barriers
-  const int njp = (wave >> 1) + 1;       // contraction j <= i < 16 wave + 16
-  u32x4 bw[2], bu[2];
-  if (active) {
+  const int njp = (wave >> 1) + 1;
+  const int ufirst = wave >= 2 ? Q : 0;  // first unit this wave takes of its own block
+  const int i2 = 16 * (3 - wave) + n;    // waves 0, 1: token of the second block
+  const bool has2 = Q > 0 && wave < 2 && 16 * (3 - wave) < len;
+  // B operands of token ti: bw[jp] (w, columns scaled by beta e^g), bu[jp] (u, by beta)
+  auto bops = [&](int ti, int nj, u32x4* bwx, u32x4* bux) {
 #pragma unroll
     for (int jp = 0; jp < 2; ++jp) {
-      if (jp >= njp) continue;
+      if (jp >= nj) continue;
       const int j0 = 32 * jp + 8 * G;
       float tw[8], tu[8];
 #pragma unroll
@@ -280,15 +293,19 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
         const f32x4 sb = *(const f32x4*)(GA + 128 + j0 + 4 * h);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float t = tval(i, j0 + 4 * h + r);
+          const float t = tval(ti, j0 + 4 * h + r);
           tw[4 * h + r] = t * sg[r];
           tu[4 * h + r] = t * sb[r];
         }
       }
-      bw[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
-      bu[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
+      bwx[jp] = u32x4{pack_bf16x2(tw[0], tw[1]), pack_bf16x2(tw[2], tw[3]), pack_bf16x2(tw[4], tw[5]), pack_bf16x2(tw[6], tw[7])};
+      if (bux != nullptr)
+        bux[jp] = u32x4{pack_bf16x2(tu[0], tu[1]), pack_bf16x2(tu[2], tu[3]), pack_bf16x2(tu[4], tu[5]), pack_bf16x2(tu[6], tu[7])};
     }
-  }
+  };
+  u32x4 bw[2], bu[2], bw2[2];
+  if (active) bops(i, njp, bw, bu);
+  if (has2) bops(i2, 2, bw2, nullptr);
   wait_lgkm0();
   block_barrier();   // every wave is done with A/T
 
@@ -304,51 +321,54 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
         *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
     }
   }
-  u32x4 wpk[KD / 32];   // w of token i, columns 32 pp + 8 G .. +7, held until the v tile lands
-  if (active) {
-#pragma unroll
-    for (int pp = 0; pp < KD / 32; ++pp) {
-      f32x4 acc[2];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jp = 0; jp < 2; ++jp)
-          if (jp < njp)
-            acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PK>(ktile, 32 * jp, pp, x, G, e, qd)),
-                               __builtin_bit_cast(bf16x8, bw[jp]), acc[x]);
-      }
-      wpk[pp] = u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
-                      pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
-    }
-  }
-  wait_vm<0>();
-  wait_lgkm0();
-  block_barrier();   // v tile in LDS
-  if (!active) return;
-
-  const lds_char* vtile = (const lds_char*)smem + L::V_OFF;
-  const bool store = i < len;
-  if (store) {
-#pragma unroll
-    for (int pp = 0; pp < KD / 32; ++pp) *(u32x4*)(wb + i * p.sw_t + 32 * pp + 8 * G) = wpk[pp];
-  }
-#pragma unroll
-  for (int pp = 0; pp < VD / 32; ++pp) {
+  // One unit: columns 32 pp + 8 G .. +7 of the lane's token, bf16-packed
+  auto wu_unit = [&](const lds_char* tile, auto pv_tag, int pp, int nj, const u32x4* b) -> u32x4 {
+    constexpr int PX = decltype(pv_tag)::value;
     f32x4 acc[2];
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       acc[x] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int jp = 0; jp < 2; ++jp)
-        if (jp < njp)
-          acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<L::PV>(vtile, 32 * jp, pp, x, G, e, qd)),
-                             __builtin_bit_cast(bf16x8, bu[jp]), acc[x]);
+        if (jp < nj)
+          acc[x] = mfma_bf16(__builtin_bit_cast(bf16x8, tr_operand<PX>(tile, 32 * jp, pp, x, G, e, qd)),
+                             __builtin_bit_cast(bf16x8, b[jp]), acc[x]);
     }
-    if (store)
-      *(u32x4*)(ub + i * p.su_t + 32 * pp + 8 * G) =
-          u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
-                pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+    return u32x4{pack_bf16x2(acc[0][0], acc[0][1]), pack_bf16x2(acc[0][2], acc[0][3]),
+                 pack_bf16x2(acc[1][0], acc[1][1]), pack_bf16x2(acc[1][2], acc[1][3])};
+  };
+  using PKT = std::integral_constant<int, L::PK>;
+  using PVT = std::integral_constant<int, L::PV>;
+  u32x4 wpk[NPW], wpk2[Q > 0 ? Q : 1];   // w results, held until the v tile lands
+  if (active) {
+#pragma unroll
+    for (int pp = 0; pp < NPW; ++pp)
+      if (pp >= ufirst) wpk[pp] = wu_unit(ktile, PKT{}, pp, njp, bw);
+  }
+  if (has2) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) wpk2[q] = wu_unit(ktile, PKT{}, q, 2, bw2);
+  }
+  wait_vm<0>();
+  wait_lgkm0();
+  block_barrier();   // v tile in LDS
+  if (has2 && i2 < len) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) *(u32x4*)(wb + i2 * p.sw_t + 32 * q + 8 * G) = wpk2[q];
+  }
+  if (!active) return;
+
+  const lds_char* vtile = (const lds_char*)smem + L::V_OFF;
+  const bool store = i < len;
+  if (store) {
+#pragma unroll
+    for (int pp = 0; pp < NPW; ++pp)
+      if (pp >= ufirst) *(u32x4*)(wb + i * p.sw_t + 32 * pp + 8 * G) = wpk[pp];
+  }
+#pragma unroll
+  for (int pp = 0; pp < VD / 32; ++pp) {
+    const u32x4 r = wu_unit(vtile, PVT{}, pp, njp, bu);
+    if (store) *(u32x4*)(ub + i * p.su_t + 32 * pp + 8 * G) = r;
   }
 }
 
