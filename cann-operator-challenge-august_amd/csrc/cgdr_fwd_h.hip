@@ -242,11 +242,11 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   return p;
 }
 
-template <int KD, int NCW, int NLW, int STAGES, bool CONTEST>
+template <int KD, int NCW, int NLW, int STAGES, int NUM>
 hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
   using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
   const unsigned grid = (unsigned)(p.helpers ? 2 * tasks : tasks);
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, CONTEST>), dim3(grid),
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, NUM>), dim3(grid),
                      dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
@@ -258,32 +258,47 @@ hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stre
   return hipGetLastError();
 }
 
-template <int KD, int NCW, int NLW, bool CONTEST>
+// NUM: the kernel's numerics mode (0 default, 1 contest fast pass, 2 contest full pass)
+template <int KD, int NCW, int NLW, int NUM>
 hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4>())
-    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, CONTEST>(p, pl.tasks, s);
+    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, NUM>(p, pl.tasks, s);
   if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3>())
-    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, CONTEST>(p, pl.tasks, s);
-  return launch_bf16<KD, NCW, NLW, 2, CONTEST>(p, pl.tasks, s);
+    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, NUM>(p, pl.tasks, s);
+  return launch_bf16<KD, NCW, NLW, 2, NUM>(p, pl.tasks, s);
 }
 
-template <int KD, int NCW, bool CONTEST>
+template <int KD, int NCW, int NUM>
 hipError_t dispatch_bf16_nlw(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, CONTEST>(p, pl, s);
-  if constexpr (!CONTEST)
-    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, CONTEST>(p, pl, s);
-  return dispatch_bf16_stages<KD, NCW, 2, CONTEST>(p, pl, s);
+  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, NUM>(p, pl, s);
+  if constexpr (NUM == 0)
+    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, NUM>(p, pl, s);
+  return dispatch_bf16_stages<KD, NCW, 2, NUM>(p, pl, s);
 }
 
-template <int KD, bool CONTEST>
+template <int KD, int NUM>
 hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (KD == 256) {
-    return dispatch_bf16_nlw<KD, 1, CONTEST>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
   } else {
-    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, CONTEST>(p, pl, s);
-    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, CONTEST>(p, pl, s);
-    return dispatch_bf16_nlw<KD, 1, CONTEST>(p, pl, s);
+    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, NUM>(p, pl, s);
+    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, NUM>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
   }
+}
+
+// Contest numerics: the fast pass (plain fp16 roundings) flags every (sequence, head) where a
+// saturating cast or nan_to_num could have changed a value; the full pass then recomputes just
+// those heads with the casts (its workgroups for unflagged heads return at once), without
+// helper workgroups, whose progress counters the fast pass has used up.
+template <int KD>
+hipError_t dispatch_contest(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  hipError_t e = dispatch_bf16<KD, 1>(p, pl, s);
+  if (e != hipSuccess) return e;
+  cgdr::FwdHParams q = p;
+  q.helpers = 0;
+  q.progress = nullptr;
+  return dispatch_bf16<KD, 2>(q, pl, s);
 }
 
 // Compile-time layout facts of the bf16 kernel instantiation a plan selects.
@@ -360,14 +375,18 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
 
 // Workspace: the head-major copy of g, needed when g's token stride is not 1 (the kernels
 // read one chunk's g row of one head as one contiguous 256-byte row), then, with helper
-// workgroups, one int32 progress counter per task.
+// workgroups, one int32 progress counter per task, then, for contest numerics, one int32 flag
+// per (sequence, head).
 size_t g_relayout_bytes(const cgdr_fwd_h_args* a) {
   if (a->g == nullptr || a->stride_g[1] == 1) return 0;
   return ((size_t)a->B * (size_t)a->H * (size_t)a->T * sizeof(float) + 255) & ~(size_t)255;
 }
 
+size_t progress_ints(const Plan& pl) { return pl.helpers ? (size_t)pl.tasks * cgdr::kProgressStride : 0; }
+size_t redo_ints(const cgdr_fwd_h_args* a, const Plan& pl) { return pl.kernel == 2 ? (size_t)(a->N * a->H) : 0; }
+
 size_t workspace_bytes_of(const cgdr_fwd_h_args* a, const Plan& pl) {
-  return g_relayout_bytes(a) + (pl.helpers ? (size_t)pl.tasks * cgdr::kProgressStride * sizeof(int32_t) : 0);
+  return g_relayout_bytes(a) + (progress_ints(pl) + redo_ints(a, pl)) * sizeof(int32_t);
 }
 
 hipError_t launch_g_relayout(const cgdr_fwd_h_args* a, float* gt, hipStream_t s) {
@@ -443,19 +462,21 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     p.sg_t = 1;
     p.sg_h = args->T;
   }
-  if (pl.helpers) {
-    p.progress = (int32_t*)((char*)workspace + g_bytes);
-    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, p.progress,
-                       (int64_t)pl.tasks * cgdr::kProgressStride);
+  const size_t nzero = progress_ints(pl) + redo_ints(args, pl);
+  if (nzero > 0) {
+    int32_t* counters = (int32_t*)((char*)workspace + g_bytes);
+    if (pl.helpers) p.progress = counters;
+    if (pl.kernel == 2) p.redo = counters + progress_ints(pl);
+    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, counters, (int64_t)nzero);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "progress reset launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "counter reset launch failed: %s", hipGetErrorString(e));
   }
   if (pl.kernel == 0) {
     switch (args->K) {
-      case 32: e = dispatch_bf16<32, false>(p, pl, s); break;
-      case 64: e = dispatch_bf16<64, false>(p, pl, s); break;
-      case 128: e = dispatch_bf16<128, false>(p, pl, s); break;
-      default: e = dispatch_bf16<256, false>(p, pl, s); break;
+      case 32: e = dispatch_bf16<32, 0>(p, pl, s); break;
+      case 64: e = dispatch_bf16<64, 0>(p, pl, s); break;
+      case 128: e = dispatch_bf16<128, 0>(p, pl, s); break;
+      default: e = dispatch_bf16<256, 0>(p, pl, s); break;
     }
   } else if (pl.kernel == 1) {
     switch (args->K) {
@@ -465,10 +486,10 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     }
   } else {
     switch (args->K) {
-      case 32: e = dispatch_bf16<32, true>(p, pl, s); break;
-      case 64: e = dispatch_bf16<64, true>(p, pl, s); break;
-      case 128: e = dispatch_bf16<128, true>(p, pl, s); break;
-      default: e = dispatch_bf16<256, true>(p, pl, s); break;
+      case 32: e = dispatch_contest<32>(p, pl, s); break;
+      case 64: e = dispatch_contest<64>(p, pl, s); break;
+      case 128: e = dispatch_contest<128>(p, pl, s); break;
+      default: e = dispatch_contest<256>(p, pl, s); break;
     }
   }
   if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));

@@ -45,7 +45,12 @@
 // where f16sat is the reference's cast_to_float16 (round to fp16, finite overflow saturates to
 // +-65504, inf and NaN pass through).  The operands are bf16, so the MFMA products are the bf16
 // GEMMs' products, accumulated in fp32 and rounded once to bf16: MM1 starts from zero instead of
-// U, and MM2 accumulates K^T vd alone, combined with the decayed state after it.
+// U, and MM2 accumulates K^T vd alone, combined with the decayed state after it.  Contest
+// numerics take two launches: a fast pass (NUM = 1) with plain fp16 roundings in place of the
+// saturating casts and nan_to_num, which tracks the largest magnitude each cast sees and flags
+// the (sequence, head) where one exceeds 65504 or is NaN; then a full pass (NUM = 2) with the
+// casts, whose workgroups return at once for unflagged heads.  Where nothing is flagged the two
+// agree bit for bit, so the result is the full pass's everywhere.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -101,6 +106,7 @@ struct FwdHParams {
   int32_t reserved;
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
                         // task (kProgressStride ints; zeroed before launch)
+  int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
 };
 
 constexpr int kProgressStride = 32;
@@ -173,6 +179,12 @@ __device__ __forceinline__ float f16_nan_to_num(float x) {
   return r != r ? 0.f : r;
 }
 __device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
+__device__ __forceinline__ float f16_rnd(float x) { return (float)(_Float16)x; }
+// bits of |x|: as unsigned integers they order like |x|, and every NaN lies above +inf
+__device__ __forceinline__ unsigned abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+__device__ __forceinline__ unsigned max3_u32(unsigned a, unsigned b, unsigned c) {
+  return __builtin_elementwise_max(a, __builtin_elementwise_max(b, c));
+}
 
 // ---------------------------------------------------------------------------------------------
 // Swizzles of 16-byte pieces inside LDS tiles (P = pieces per row).  Each is chosen so that the
@@ -320,9 +332,13 @@ constexpr int bf16_max_stages() {
   return bf16_config_ok<KD, NCW, NLW, 4>() ? 4 : bf16_config_ok<KD, NCW, NLW, 3>() ? 3 : 2;
 }
 
-template <int KD, int NCW, int NLW, int STAGES, bool CONTEST = false>
+// NUM: 0 default numerics; 1 contest, fast pass (plain fp16 roundings, flags the heads where a
+// saturating cast or nan_to_num could matter); 2 contest, full pass (the saturating casts, only
+// for flagged heads).
+template <int KD, int NCW, int NLW, int STAGES, int NUM = 0>
 __global__ void __launch_bounds__(64 * (NCW + NLW + NCW + 1))
 cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
+  constexpr bool CONTEST = NUM != 0, FULL = NUM == 2;
   using L = Bf16Layout<KD, NCW, NLW, STAGES>;
   constexpr int VT = L::VT, P = L::P;
   constexpr int KT = KD / 16;   // MM2 output tiles (rows of S)
@@ -345,6 +361,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   }
   if (task_id >= p.n_tasks) return;   // uniform per workgroup
   const Task tk = decode_task(p, task_id);
+  if constexpr (FULL)
+    if (p.redo[(int64_t)tk.n * p.H + tk.head] == 0) return;   // uniform: the fast pass was exact
   const int NC = tk.nc;
   const int vbase = tk.vtile * VT;
   const int hk = tk.head / p.head_ratio;
@@ -484,6 +502,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const int g = lane >> 4, n = lane & 15;
     const int vcol = vbase + 16 * wave + n;      // value column owned by this lane
     f32x4 S[KT];
+    // contest fast pass: largest |x| (as bits) of the values whose saturating cast must be a
+    // plain rounding (<= 65504 = 0x477fe000, not NaN), and of the state (not NaN)
+    unsigned mbits = 0, nbits = 0;
     if (p.h0 != nullptr) {
       const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
 #pragma unroll
@@ -591,11 +612,21 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           acc[tt] = mfma_bf16(__builtin_bit_cast(bf16x8, wop[tt][kb]), __builtin_bit_cast(bf16x8, Sw[kb]), acc[tt]);
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
-        if constexpr (CONTEST) {
-          // hd = f16sat(f16sat(S) a) kept as bf16(hd); S becomes the K^T Vd accumulator
+        if constexpr (FULL) {
+          // hd = f16sat(f16sat(S) a), kept as bf16(hd); S becomes the K^T Vd accumulator
 #pragma unroll
           for (int r = 0; r < 2; ++r)
             hdp[kt][r] = pack_bf16x2(f16_sat(f16_sat(S[kt][2 * r]) * a), f16_sat(f16_sat(S[kt][2 * r + 1]) * a));
+          S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (CONTEST) {
+          // While |f16(S) a| <= 65504 and is not NaN, both casts are plain fp16 roundings (an S
+          // beyond the fp16 range makes the product inf or NaN).
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const float p0 = f16_rnd(S[kt][2 * r]) * a, p1 = f16_rnd(S[kt][2 * r + 1]) * a;
+            mbits = max3_u32(mbits, abs_bits(p0), abs_bits(p1));
+            hdp[kt][r] = pack_bf16x2(f16_rnd(p0), f16_rnd(p1));
+          }
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[kt] = S[kt] * a;
@@ -613,6 +644,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       // Phase 3: epilogue of token block 0 (v_new staging, Vd = bf16(Vn * gamma)).
       u32x4* sv = (u32x4*)(smem + L::SV_OFF + par * L::SV_BYTES);
       const int vrow = 16 * wave + n;
+      // Contest: the saturating casts in the full pass; plain fp16 roundings in the fast pass,
+      // which give the same values while u - ws and v16 gamma stay within +-65504 and are not
+      // NaN (a NaN or infinite ws, or a u beyond the fp16 range, makes u - ws fail that).
       auto epilogue = [&](int tb) -> bf16x8 {
         u32x4 pv, pd;
 #pragma unroll
@@ -624,10 +658,20 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             const u32x2 ur = uraw[2 * tb + hh];
             const float u0 = r == 0 ? bf16_lo(ur[0]) : bf16_lo(ur[1]);
             const float u1 = r == 0 ? bf16_hi(ur[0]) : bf16_hi(ur[1]);
-            const float x0 = f16_sat(f16_sat(u0) - f16_nan_to_num(-bf16_rnd(v0)));
-            const float x1 = f16_sat(f16_sat(u1) - f16_nan_to_num(-bf16_rnd(v1)));
-            pv[j] = pack_bf16x2(x0, x1);
-            pd[j] = pack_bf16x2(f16_sat(x0 * gm[tb][hh][r]), f16_sat(x1 * gm[tb][hh][r + 1]));
+            if constexpr (FULL) {
+              const float x0 = f16_sat(f16_sat(u0) - f16_nan_to_num(-bf16_rnd(v0)));
+              const float x1 = f16_sat(f16_sat(u1) - f16_nan_to_num(-bf16_rnd(v1)));
+              pv[j] = pack_bf16x2(x0, x1);
+              pd[j] = pack_bf16x2(f16_sat(x0 * gm[tb][hh][r]), f16_sat(x1 * gm[tb][hh][r + 1]));
+            } else {
+              const float y0 = f16_rnd(u0) - f16_rnd(-bf16_rnd(v0));
+              const float y1 = f16_rnd(u1) - f16_rnd(-bf16_rnd(v1));
+              const float x0 = f16_rnd(y0), x1 = f16_rnd(y1);
+              const float z0 = x0 * gm[tb][hh][r], z1 = x1 * gm[tb][hh][r + 1];
+              mbits = max3_u32(mbits, max3_u32(abs_bits(y0), abs_bits(y1), abs_bits(z0)), abs_bits(z1));
+              pv[j] = pack_bf16x2(x0, x1);
+              pd[j] = pack_bf16x2(f16_rnd(z0), f16_rnd(z1));
+            }
           } else {
             pv[j] = pack_bf16x2(v0, v1);
             pd[j] = pack_bf16x2(v0 * gm[tb][hh][r], v1 * gm[tb][hh][r + 1]);
@@ -656,14 +700,20 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[kt]), Vd1, S[kt]);
       if constexpr (CONTEST) {
-        // S = bf16(bf16(hd) + bf16(nan_to_num(fp16(bf16(K^T Vd)))))
+        // S = bf16(bf16(hd) + bf16(nan_to_num(fp16(bf16(K^T Vd))))).  nan_to_num changes only a
+        // NaN, which the fast pass leaves in the new state, where the check finds it.
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const unsigned hw = hdp[kt][r >> 1];
             const float hd = (r & 1) ? bf16_hi(hw) : bf16_lo(hw);
-            S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[kt][r]))));
+            if constexpr (FULL) {
+              S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[kt][r]))));
+            } else {
+              S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_rnd(bf16_rnd(S[kt][r]))));
+              nbits = __builtin_elementwise_max(nbits, abs_bits(S[kt][r]));
+            }
           }
       }
       wait_lgkm0();
@@ -678,6 +728,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       });
     }
 
+    if constexpr (NUM == 1) {
+      // flag the head for the full pass (every wave and V-tile of it writes the same 1)
+      if (__any(mbits > 0x477fe000u || nbits > 0x7f800000u) && lane == 0)
+        p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
+    }
     if (p.final_state != nullptr) {
       const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
 #pragma unroll

@@ -71,7 +71,8 @@ typedef enum cgdr_dtype {
  *   CGDR_NUMERICS_CONTEST: bf16 inputs only; the contest reference run() /
  *     run_reference (docs/problem.txt:81-167, code/tests/golden/generate_golden.py:350-440):
  *     bf16 state, bf16 GEMM outputs, saturating fp16 casts and nan_to_num after each GEMM,
- *     on the same pipelined kernel. */
+ *     on the same pipelined kernel (a fast pass with plain fp16 roundings, then the casts
+ *     again for the heads where one could matter; same results). */
 typedef enum cgdr_numerics {
   CGDR_NUMERICS_DEFAULT = 0,
   CGDR_NUMERICS_CONTEST = 1
@@ -116,7 +117,8 @@ typedef struct cgdr_fwd_h_args {
 /* Phase 1 (host only, no device access): validate the arguments and report the
  * workspace the launch needs: B*H*T*4 bytes rounded up to 256 (a head-major copy of g) when
  * g is given with a token stride other than 1, plus 128 bytes per task (progress counters)
- * when the plan uses helper workgroups; 0 when neither applies.
+ * when the plan uses helper workgroups, plus N*H*4 bytes (one flag per sequence and head)
+ * with CGDR_NUMERICS_CONTEST; 0 when none applies.
  * Replaces aclnnChunkGatedDeltaRuleFwdHGetWorkspaceSize. */
 cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* workspace_bytes);
 

@@ -124,6 +124,17 @@ def test_token_major_g_needs_head_major_workspace(lib):
     assert _status(_with_g(_args(varlen=[0, 61, 64], T=64, H=3, Hg=1)))[1] == 3 * 64 * 4 + 24 * 128
 
 
+def test_contest_numerics_need_one_flag_per_head(lib):
+    # contest numerics: one int32 flag per (sequence, head) for the full pass, after the
+    # progress lines of any helper workgroups
+    a = _args(H=3, Hg=1)   # 12 tasks: no helper workgroups
+    a.numerics = _abi.CGDR_NUMERICS_CONTEST
+    assert _status(a) == (_abi.CGDR_OK, 3 * 4)
+    a = _args(varlen=[0, 61, 64], T=64, H=3, Hg=1)
+    a.numerics = _abi.CGDR_NUMERICS_CONTEST
+    assert _status(a)[1] == 24 * 128 + 2 * 3 * 4
+
+
 def test_launch_rejects_missing_or_short_workspace(lib):
     # host-side check before anything is enqueued, so it runs without a GPU
     a = _with_g(_args())
