@@ -47,10 +47,10 @@
 // GEMMs' products, accumulated in fp32 and rounded once to bf16: MM1 starts from zero instead of
 // U, and MM2 accumulates K^T vd alone, combined with the decayed state after it.  Contest
 // numerics take two launches: a fast pass (NUM = 1) with plain fp16 roundings in place of the
-// saturating casts and nan_to_num, which tracks the largest magnitude each cast sees and flags
-// the (sequence, head) where one exceeds 65504 or is NaN; then a full pass (NUM = 2) with the
-// casts, whose workgroups return at once for unflagged heads.  Where nothing is flagged the two
-// agree bit for bit, so the result is the full pass's everywhere.
+// saturating casts and nan_to_num, where the store waves (h snapshots, v_new), the gate wave
+// (gates, decay) and the compute waves (final state, once) flag the (sequence, head) whose
+// values leave the range where the two agree; then a full pass (NUM = 2) with the casts, whose
+// workgroups return at once for unflagged heads.  So the result is the full pass's everywhere.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -180,10 +180,12 @@ __device__ __forceinline__ float f16_nan_to_num(float x) {
 }
 __device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float f16_rnd(float x) { return (float)(_Float16)x; }
-// bits of |x|: as unsigned integers they order like |x|, and every NaN lies above +inf
-__device__ __forceinline__ unsigned abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
-__device__ __forceinline__ unsigned max3_u32(unsigned a, unsigned b, unsigned c) {
-  return __builtin_elementwise_max(a, __builtin_elementwise_max(b, c));
+// Running maximum of |x| over the two bf16 of a word, per half (v_pk_max_u16): the bits of
+// |x| order like |x| as unsigned integers, and every NaN lies above +inf (0x7f80).
+__device__ __forceinline__ unsigned pk_absmax_bf16(unsigned acc, unsigned w) {
+  typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
+  return __builtin_bit_cast(unsigned, __builtin_elementwise_max(__builtin_bit_cast(u16x2, acc),
+                                                                __builtin_bit_cast(u16x2, w & 0x7fff7fffu)));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -371,6 +373,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   // Gate factors of chunk c into stage st from its raw g row (one wave; gv = g of token
   // `lane` of the chunk): gamma_t = safe_exp(g_last - g_t) for t < len, 0 for padded rows,
   // and a = exp(g_last) in slot 64.  No gating: gamma = 1, a = 1.
+  bool gbad = false;   // contest fast pass, gate wave: a gate above 1 or NaN
   auto gates = [&](int c, int st, float gv) {
     const int64_t rem = tk.len - (int64_t)c * kChunk;
     const int len = rem < kChunk ? (int)rem : kChunk;
@@ -382,6 +385,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         // fp16 gate of every token and fp16 exp of the fp16 g_last (generate_golden.py:409-416)
         gamma = lane < len ? f16_sat(expf(glast - gv)) : 0.f;
         a = (float)(_Float16)expf(f16_sat(glast));
+        gbad |= !(gamma <= 1.f) || !(a <= 1.f);   // the fast pass is exact for gates in [0, 1]
       } else {
         gamma = lane < len ? safe_exp(glast - gv) : 0.f;
         a = expf(glast);
@@ -502,9 +506,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const int g = lane >> 4, n = lane & 15;
     const int vcol = vbase + 16 * wave + n;      // value column owned by this lane
     f32x4 S[KT];
-    // contest fast pass: largest |x| (as bits) of the values whose saturating cast must be a
-    // plain rounding (<= 65504 = 0x477fe000, not NaN), and of the state (not NaN)
-    unsigned mbits = 0, nbits = 0;
+
     if (p.h0 != nullptr) {
       const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
 #pragma unroll
@@ -619,12 +621,10 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             hdp[kt][r] = pack_bf16x2(f16_sat(f16_sat(S[kt][2 * r]) * a), f16_sat(f16_sat(S[kt][2 * r + 1]) * a));
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else if constexpr (CONTEST) {
-          // While |f16(S) a| <= 65504 and is not NaN, both casts are plain fp16 roundings (an S
-          // beyond the fp16 range makes the product inf or NaN).
+          // fast pass: plain fp16 roundings (exact while |S| <= 65504 and 0 <= a <= 1)
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
             const float p0 = f16_rnd(S[kt][2 * r]) * a, p1 = f16_rnd(S[kt][2 * r + 1]) * a;
-            mbits = max3_u32(mbits, abs_bits(p0), abs_bits(p1));
             hdp[kt][r] = pack_bf16x2(f16_rnd(p0), f16_rnd(p1));
           }
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -645,8 +645,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       u32x4* sv = (u32x4*)(smem + L::SV_OFF + par * L::SV_BYTES);
       const int vrow = 16 * wave + n;
       // Contest: the saturating casts in the full pass; plain fp16 roundings in the fast pass,
-      // which give the same values while u - ws and v16 gamma stay within +-65504 and are not
-      // NaN (a NaN or infinite ws, or a u beyond the fp16 range, makes u - ws fail that).
+      // which give the same values while v16 = fp16(u - ws) is finite (a NaN or infinite ws, or
+      // a u beyond the fp16 range, makes it inf or NaN) and the gates are at most 1.
       auto epilogue = [&](int tb) -> bf16x8 {
         u32x4 pv, pd;
 #pragma unroll
@@ -668,7 +668,6 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
               const float y1 = f16_rnd(u1) - f16_rnd(-bf16_rnd(v1));
               const float x0 = f16_rnd(y0), x1 = f16_rnd(y1);
               const float z0 = x0 * gm[tb][hh][r], z1 = x1 * gm[tb][hh][r + 1];
-              mbits = max3_u32(mbits, max3_u32(abs_bits(y0), abs_bits(y1), abs_bits(z0)), abs_bits(z1));
               pv[j] = pack_bf16x2(x0, x1);
               pd[j] = pack_bf16x2(f16_rnd(z0), f16_rnd(z1));
             }
@@ -701,7 +700,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       for (int kt = 0; kt < KT; ++kt) S[kt] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[kt]), Vd1, S[kt]);
       if constexpr (CONTEST) {
         // S = bf16(bf16(hd) + bf16(nan_to_num(fp16(bf16(K^T Vd))))).  nan_to_num changes only a
-        // NaN, which the fast pass leaves in the new state, where the check finds it.
+        // NaN, which the fast pass leaves in the new state (seen in the next h snapshot, or in
+        // the final state below).
 #pragma unroll
         for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
@@ -712,7 +712,6 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
               S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[kt][r]))));
             } else {
               S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_rnd(bf16_rnd(S[kt][r]))));
-              nbits = __builtin_elementwise_max(nbits, abs_bits(S[kt][r]));
             }
           }
       }
@@ -729,9 +728,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
 
     if constexpr (NUM == 1) {
-      // flag the head for the full pass (every wave and V-tile of it writes the same 1)
-      if (__any(mbits > 0x477fe000u || nbits > 0x7f800000u) && lane == 0)
-        p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
+      bool bad = false;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= S[kt][r] != S[kt][r];
+      if (__any(bad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
     }
     if (p.final_state != nullptr) {
       const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
@@ -883,6 +885,10 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
     __bf16* vbase_ptr = p.v_new == nullptr ? nullptr
                        : (__bf16*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h + vbase;
+    // contest fast pass: largest |h| and |v_new| seen.  The fast pass is exact while every state
+    // entering a chunk (the h snapshot, bf16 = S) is within +-65504 and every v_new is finite;
+    // both hold when no bf16 exceeds 65280 (0x477f): the next bf16 is 65536.
+    unsigned amax = 0;
 
     auto store_chunk = [&](int c) {
       const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
@@ -904,12 +910,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
           hv[2 * half] = x[0] ^ 0x80008000u;       // staged as bf16(-S)
           hv[2 * half + 1] = x[1] ^ 0x80008000u;
+          if constexpr (NUM == 1) amax = pk_absmax_bf16(pk_absmax_bf16(amax, x[0]), x[1]);
         }
         *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;
       }
-      if (vbase_ptr != nullptr) {
+      if (vbase_ptr != nullptr || NUM == 1) {
         const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
-        __bf16* vdst = vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
+        __bf16* vdst = vbase_ptr == nullptr ? nullptr : vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
         constexpr int UNITS_V = 4 * (VT / 8);
 #pragma unroll
         for (int m = 0; m < (UNITS_V + 3) / 4; ++m) {
@@ -928,7 +935,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             vv[2 * half] = x[0];
             vv[2 * half + 1] = x[1];
           }
-          if (t0 + i < len) *(u32x4*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = vv;
+          if (t0 + i < len) {
+            if (vbase_ptr != nullptr) *(u32x4*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = vv;
+            if constexpr (NUM == 1)
+              amax = pk_absmax_bf16(pk_absmax_bf16(pk_absmax_bf16(pk_absmax_bf16(amax, vv[0]), vv[1]), vv[2]), vv[3]);
+          }
         }
       }
     };
@@ -955,6 +966,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
     if (NC > 0) store_chunk(NC - 1);
     if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
+    if constexpr (NUM == 1)
+      if (__any((amax & 0xffffu) > 0x477fu || (amax >> 16) > 0x477fu) && lane == 0)
+        p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
   } else if (wave == NCW + L::NSW + NLW) {
     // ------------------------------------------------------------------ gate wave
     // Loads the raw g rows itself, with ordinary loads into registers two chunks ahead, and
@@ -981,6 +995,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       wait_lgkm0();
       block_barrier();   // B_c
     }
+    if constexpr (NUM == 1)
+      if (__any(gbad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
   }
 }
 

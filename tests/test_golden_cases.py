@@ -281,6 +281,33 @@ def test_contest_kernel_saturation(dev):
 
 
 @pytest.mark.gpu
+def test_contest_kernel_rising_gates_and_large_state(dev):
+    """Gates above 1 (g rising inside a chunk) on one head, an initial state beyond the fp16
+    range on another, ordinary values on the third: the heads that need the saturating casts
+    are recomputed with them, and all three follow the oracle."""
+    print("[contest] rising gates, large state", flush=True)
+    rng = np.random.default_rng(7)
+    T, HV, HK, D = 200, 3, 3, 128
+    k = O.bf16_round((rng.standard_normal((1, T, HK, D)) / np.sqrt(D)).astype(np.float32))
+    w = O.bf16_round((rng.standard_normal((1, HV, T, D)) / np.sqrt(D)).astype(np.float32))
+    u = O.bf16_round(rng.standard_normal((1, HV, T, D)).astype(np.float32))
+    g = np.zeros((1, HV, T), np.float32)
+    for i0 in range(0, T, 64):
+        n = min(64, T - i0)
+        g[0, :, i0:i0 + n] = -0.05 * np.arange(1, n + 1, dtype=np.float32)
+    g[0, 0, :] *= -0.2                   # head 0: rising g, gates up to e^0.6
+    h0 = O.bf16_round((rng.standard_normal((1, HV, D, D)) * 0.1).astype(np.float32))
+    h0[0, 1, :4, :4] = 7.0e4             # head 1: state entries above 65504
+    cu = np.array([0, T], np.int64)
+    a = dict(input_k=k, input_w=w, input_u=u, input_g=g, input_cu_seqlens=cu, input_initial_state=h0)
+    got = _run_contest(dev, a)
+    ref = O.fwd_h_o2(k, w, u, g, h0, cu)
+    for name, x, r in zip(("h", "v", "final"), got, ref):
+        same = (x == r) | (np.isnan(x) & np.isnan(r))
+        assert same.mean() >= O2_MIN_EXACT, (name, same.mean())
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("case", [c for c in CASES if c.name in ("long_1024_single", "grouped_heads_packed")],
                          ids=lambda c: c.name)
 def test_runner_contest_mode(dev, case, tmp_path):
