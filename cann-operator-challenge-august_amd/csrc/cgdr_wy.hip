@@ -15,9 +15,6 @@ namespace {
 using cgdr_host::fail;
 
 constexpr int64_t kMaxUnits = (int64_t(1) << 31) - 1;
-// Workgroups between a unit and the later unit whose k rows it prefetches into L2 (a multiple
-// of the 8 XCDs; at K = V = 128 registers allow three workgroups per CU, 768 on the chip).
-constexpr int kPrefetchLead = 384;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 bool dim_ok(int64_t d) { return d == 32 || d == 64 || d == 128 || d == 256; }
@@ -117,7 +114,6 @@ extern "C" cgdr_status cgdr_wy_launch(const cgdr_wy_args* a, void* stream) {
   p.sw_b = a->stride_w[0]; p.sw_t = a->stride_w[1]; p.sw_h = a->stride_w[2];
   p.su_b = a->stride_u[0]; p.su_t = a->stride_u[1]; p.su_h = a->stride_u[2];
   p.sc_b = a->stride_g_cumsum[0]; p.sc_t = a->stride_g_cumsum[1]; p.sc_h = a->stride_g_cumsum[2];
-  p.pf_lead = kPrefetchLead;
   const int64_t units = a->B * a->NT * a->H;
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;

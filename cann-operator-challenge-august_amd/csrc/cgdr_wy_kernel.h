@@ -14,7 +14,7 @@
 // Phases, separated by workgroup barriers:
 //   0  DMA of the k tile into LDS; wave 0 forms g (each lane sums a_0..a_i in order, which is
 //      the sequential cumsum bit for bit), beta e^g and beta.  Then each wave touches its share
-//      of this unit's v rows and of a later unit's k rows into L2.
+//      of this unit's v rows into L2.
 //   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, operands read from the k tile),
 //      A written to LDS in fp32
 //   2  T: each wave inverts its own 16x16 diagonal block by forward substitution right after
@@ -55,7 +55,6 @@ struct WyParams {
   int64_t sw_b, sw_t, sw_h;
   int64_t su_b, su_t, su_h;
   int64_t sc_b, sc_t, sc_h;
-  int32_t pf_lead;   // L2 prefetch: workgroups ahead (a multiple of 8), 0 = off
 };
 
 template <int KD, int VD>
@@ -143,10 +142,7 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   wait_lgkm0();
   block_barrier();
 
-  // ---- L2 prefetch: the v rows of this unit (loaded into LDS in phase 3) and the k rows of the
-  // unit of workgroup blockIdx + pf_lead.  Workgroups are dealt to the 8 XCDs round-robin, so
-  // with pf_lead a multiple of 8 that unit runs on this XCD, about pf_lead / (resident
-  // workgroups) unit lifetimes from now, and finds its rows in this XCD's L2.  One 4-byte
+  // ---- L2 prefetch of this unit's v rows, which phase 3 loads into LDS: one 4-byte
   // direct-to-LDS load per 128-byte line, landing in the a[] slot of the g area (not read after
   // phase 0); each wave drains its own before the barrier ahead of phase 3.
   {
@@ -157,21 +153,6 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
       if ((LK + m) % 4 != wave) continue;
       const int t = 64 * m + lane, r = t / LV;
       if (r < len) dma_b32_addr((const char*)vb + r * p.sv_t * 2 + 128 * (t % LV), trash);
-    }
-    if (p.pf_lead > 0 && (int64_t)blockIdx.x + p.pf_lead < (int64_t)gridDim.x) {
-      int64_t u2 = xcd_remap(blockIdx.x + p.pf_lead, gridDim.x);
-      const int head2 = (int)(u2 % p.H);
-      u2 /= p.H;
-      const ChunkRange cr2 = chunk_range(p.T, p.N, p.cu_seqlens, p.chunk_indices, u2 % p.NT);
-      const int b2 = (int)(u2 / p.NT);
-      const int len2 = __builtin_amdgcn_readfirstlane(cr2.len);
-      const char* k2 = (const char*)p.k + 2 * (b2 * p.sk_b + cr2.start * p.sk_t + (head2 / (p.H / p.Hg)) * p.sk_h);
-#pragma unroll
-      for (int m = 0; m < LK; ++m) {
-        if (m % 4 != wave) continue;
-        const int t = 64 * m + lane, r = t / LK;
-        if (r < len2) dma_b32_addr(k2 + r * p.sk_t * 2 + 128 * (t % LK), trash);
-      }
     }
   }
 
