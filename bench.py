@@ -385,7 +385,7 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = B * T * args.steps / wall
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
-    plan = cgdr_amd.plan(k, u)
+    plan = cgdr_amd.plan(k, u, numerics=args.numerics)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "cgdr_fwd_h_bf16_T32768_H32_hbm_traffic.md")

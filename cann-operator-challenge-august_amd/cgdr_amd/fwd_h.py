@@ -252,7 +252,7 @@ def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_S
 
 
 def plan(k: torch.Tensor, u: torch.Tensor, H: int | None = None, N: int | None = None,
-         cu_seqlens_len: int | None = None) -> dict:
+         cu_seqlens_len: int | None = None, numerics: str = "default") -> dict:
     """Launch plan the library picks for token-major inputs of these shapes (host only)."""
     B, T, Hg, K = k.shape
     H = u.shape[-2] if H is None else H
@@ -273,5 +273,6 @@ def plan(k: torch.Tensor, u: torch.Tensor, H: int | None = None, N: int | None =
     a.stride_u[:] = [T * H * V, H * V, V]
     NT = a.NT
     a.stride_h[:] = [NT * H * K * V, H * K * V, K * V]
+    a.numerics = _NUMERICS[numerics]
     p = _abi.get_plan(a)
     return {f: getattr(p, f) for f, _ in _abi.FwdHPlan._fields_}
