@@ -328,8 +328,8 @@ def main():
                          "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build's path has no multi-GPU component "
-              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        print(f"bench.py measures one GPU: the FwdH path runs on one GPU and has no multi-GPU "
+              f"component (--gpus {args.gpus} requested)", file=sys.stderr)
         sys.exit(2)
 
     import torch
