@@ -56,7 +56,7 @@ typedef enum cgdr_status {
   CGDR_OK = 0,
   CGDR_ERR_NULLPTR = 1,     /* a required pointer is null                         */
   CGDR_ERR_INVALID = 2,     /* shapes / strides / sizes are inconsistent          */
-  CGDR_ERR_UNSUPPORTED = 3, /* valid request this build does not implement         */
+  CGDR_ERR_UNSUPPORTED = 3, /* valid request the library does not implement         */
   CGDR_ERR_LAUNCH = 4       /* the HIP runtime rejected the launch                 */
 } cgdr_status;
 

@@ -1,6 +1,6 @@
 """CPU oracle for the ChunkGatedDeltaRuleFwdH chunk recurrence (numpy).
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker: only ``tests/``,
+TEST INFRASTRUCTURE ONLY.  This module is the reference for the tests: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  The product path (the HIP library behind ``include/cgdr_fwd_h.h``)
 never calls into it and never falls back to it.

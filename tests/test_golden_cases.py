@@ -5,7 +5,7 @@ Tolerances, written per check:
   * first h snapshot of every sequence == initial_state (or 0): bit-exact;
   * h, v_new, final_state: max |error| <= 1% of the tensor's max |golden|.  O2 keeps the state
     in bf16 between chunks (docs/problem.txt:137-167) where the Triton kernel, this oracle and
-    this build keep it in fp32, so h and final differ from the golden by about one bf16 ulp of
+    the default numerics of the library keep it in fp32, so h and final differ from the golden by about one bf16 ulp of
     the state; v_new additionally within rtol=2e-2, atol=2e-3 for all but 0.1% of elements.
 """
 
