@@ -281,6 +281,50 @@ def test_contest_kernel_saturation(dev):
 
 
 @pytest.mark.gpu
+def test_contest_kernel_without_v_new_output(dev):
+    """Token-major calls, u beyond the fp16 range on one head: that shows first in the staged
+    v_new, which the fast pass checks whether or not v_new is an output.  With v_new requested
+    the saturated values (bf16(65504) = 65536, where the fast pass alone would leave inf) follow
+    the oracle; without it, h and the final state are bit for bit the same."""
+    import cgdr_amd
+    print("[contest] no v_new output", flush=True)
+    rng = np.random.default_rng(9)
+    T, HV, HK, D = 150, 2, 1, 128
+    k = O.bf16_round((rng.random((1, T, HK, D)) * 2 - 1).astype(np.float32))
+    w = O.bf16_round(((rng.random((1, T, HV, D)) * 2 - 1) / D).astype(np.float32))
+    u = O.bf16_round((rng.random((1, T, HV, D)) * 2 - 1).astype(np.float32))
+    u[0, 70:90, 1] *= 1.2e5                 # head 1: u beyond the fp16 range
+    g = np.zeros((1, T, HV), np.float32)
+    for i0, i1 in ((0, 64), (64, 128), (128, 150)):
+        g[0, i0:i1] = -0.02 * np.arange(1, i1 - i0 + 1, dtype=np.float32)[:, None]
+    t = lambda x, dt: torch.from_numpy(np.ascontiguousarray(x)).to(device=dev, dtype=dt)
+
+    def call(save_v):
+        out = cgdr_amd.chunk_gated_delta_rule_fwd_h(
+            t(k, torch.bfloat16), t(w, torch.bfloat16), t(u, torch.bfloat16), g=t(g, torch.float32),
+            output_final_state=True, save_new_value=save_v, final_state_dtype=torch.bfloat16,
+            numerics="contest")
+        torch.cuda.synchronize()
+        return out
+
+    h1, v1, f1 = call(True)
+    h0, v0, f0 = call(False)
+    assert v0 is None
+    hm = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))   # [1,T,H,D] -> [1,H,T,D]
+    ref = O.fwd_h_o2(k, hm(w), hm(u), np.ascontiguousarray(g.transpose(0, 2, 1)), None, None)
+    gv = hm(v1.float().cpu().numpy())
+    assert (np.abs(gv[0, 1]) == 65536).any() and not np.isinf(gv).any()
+    same = (gv == ref[1]) | (np.isnan(gv) & np.isnan(ref[1]))
+    assert same.mean() >= O2_MIN_EXACT, same.mean()
+    # the snapshots before the saturated tokens reach the state follow the oracle (chunk 2 holds
+    # states of ~1e6 built from +-65504 values, where the GEMMs' fp32 summation order shows)
+    gh = h1.float().cpu().numpy().transpose(0, 2, 1, 3, 4)          # [1,NT,H,K,V] -> [1,H,NT,K,V]
+    assert (gh[:, :, :2] == ref[0][:, :, :2]).mean() >= O2_MIN_EXACT
+    assert torch.equal(h0.view(torch.int16), h1.view(torch.int16))
+    assert torch.equal(f0.view(torch.int16), f1.view(torch.int16))
+
+
+@pytest.mark.gpu
 def test_contest_kernel_rising_gates_and_large_state(dev):
     """Gates above 1 (g rising inside a chunk) on one head, an initial state beyond the fp16
     range on another, ordinary values on the third: the heads that need the saturating casts
