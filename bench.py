@@ -67,33 +67,73 @@ def make_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
     return k, w, u, g
 
 
-def cpu_baseline(torch, k, w, u, g, sample_heads: int, repeats: int = 3):
-    """Time the numpy oracle (exact fp32 chunk loop) on the host, on a head subset."""
+def head_parallel_cpu(run, n_heads: int, group: int, T: int, repeats: int, what: str):
+    """Time an oracle over heads [0, n_heads) of T tokens on the host's cores.
+
+    Heads are split over worker threads that each run single-threaded BLAS: the oracle's
+    per-chunk GEMMs are too small for multi-threaded BLAS, which ran slower than one thread.
+    The worker count is chosen by a sweep on the first min(T, 4096) tokens; the chosen count
+    is then timed on all T tokens (median of `repeats` after that warm-up).  `run(lo, hi, t)`
+    runs the oracle on heads [lo, hi) and the first t tokens; `group` keeps head slices whole
+    multiples of the heads that share a key head."""
+    from concurrent.futures import ThreadPoolExecutor
+
     from threadpoolctl import threadpool_limits
 
-    from oracle import cgdr_oracle as O
-
     cores = len(os.sched_getaffinity(0))
-    hs = slice(0, sample_heads)
-    kh = k[:, :, : max(1, sample_heads * k.shape[2] // w.shape[2])].float().cpu().numpy()
-    wh = w[:, :, hs].float().cpu().numpy()
-    uh = u[:, :, hs].float().cpu().numpy()
-    gh = g[:, :, hs].float().cpu().numpy()
-    times = []
-    with threadpool_limits(cores):
-        O.fwd_h(kh[:, :2048], wh[:, :2048], uh[:, :2048], gh[:, :2048])      # warm-up
-        for i in range(repeats):
+    counts = [c for c in (1, 2, 4, 8, 16, 32, 64) if c <= min(cores, n_heads // group)]
+
+    def timed(nw, t):
+        units = n_heads // group
+        cuts = [group * (units * i // nw) for i in range(nw + 1)]
+        with ThreadPoolExecutor(nw) as ex:
             t0 = time.perf_counter()
-            O.fwd_h(kh, wh, uh, gh)
-            times.append(time.perf_counter() - t0)
+            list(ex.map(lambda i: run(cuts[i], cuts[i + 1], t), range(nw)))
+            return time.perf_counter() - t0
+
+    ts = min(T, 4096)
+    sweep = {}
+    with threadpool_limits(1):
+        timed(counts[-1], ts)   # warm-up (thread pools, first touch of the inputs)
+        for nw in counts:
+            sweep[nw] = timed(nw, ts)
+        best = min(sweep, key=sweep.get)
+        progress(f"cpu baseline: {best} worker threads fastest on {ts} tokens "
+                 f"({', '.join(f'{c}: {s:.2f} s' for c, s in sweep.items())})")
+        times = []
+        for i in range(repeats):
+            times.append(timed(best, T))
             progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
     t = statistics.median(times)
-    tokens = k.shape[0] * k.shape[1]
-    frac = sample_heads / w.shape[2]
-    return dict(value=tokens * frac / t, unit="tokens/s", cores=cores, kind="port",
-                sample=f"numpy oracle (exact fp32 chunk loop), B=1 T={k.shape[1]} on {sample_heads} of "
-                       f"{w.shape[2]} heads, median of {repeats}; value scaled to all heads "
+    return dict(t=t, cores=best, host_cores=cores, sample_tokens=ts,
+                single_thread_tokens_per_s=ts / sweep[1] if 1 in sweep else None,
+                sample=f"{what}, T={T} on {n_heads} heads split over {best} worker threads of one BLAS "
+                       f"thread each (fastest of {counts} on {ts} tokens), median of {repeats} "
                        f"({t:.2f} s per run)")
+
+
+def cpu_report(r, tokens: int, frac: float):
+    """The cpu_baseline object from a head_parallel_cpu result, value scaled to all heads."""
+    out = dict(value=tokens * frac / r["t"], unit="tokens/s", cores=r["cores"], kind="port",
+               sample=r["sample"] + ("; value scaled to all heads" if frac < 1 else ""),
+               host_cores=r["host_cores"])
+    if r["single_thread_tokens_per_s"] is not None:
+        out["single_thread"] = {"value": r["single_thread_tokens_per_s"] * frac, "unit": "tokens/s", "cores": 1,
+                                "sample": f"same oracle on one thread, first {r['sample_tokens']} tokens"}
+    return out
+
+
+def cpu_baseline(torch, k, w, u, g, sample_heads: int, repeats: int = 3):
+    """Time the numpy oracle (exact fp32 chunk loop) on the host, on a head subset."""
+    from oracle import cgdr_oracle as O
+
+    H, Hg = w.shape[2], k.shape[2]
+    r = H // Hg
+    kh = k[:, :, : max(1, sample_heads // r)].float().cpu().numpy()
+    wh, uh, gh = (x[:, :, :sample_heads].float().cpu().numpy() for x in (w, u, g))
+    run = lambda lo, hi, t: O.fwd_h(kh[:, :t, lo // r:hi // r], wh[:, :t, lo:hi], uh[:, :t, lo:hi], gh[:, :t, lo:hi])
+    res = head_parallel_cpu(run, sample_heads, r, k.shape[1], repeats, "numpy oracle (exact fp32 chunk loop), B=1")
+    return cpu_report(res, k.shape[0] * k.shape[1], sample_heads / H)
 
 
 def chunk_o_bytes(B, T, H, Hg, K, V, NT, s=2):
@@ -120,27 +160,17 @@ def make_chunk_o_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
 
 
 def chunk_o_cpu_baseline(torch, q, k, v, h, g, sample_heads: int, repeats: int = 3):
-    from threadpoolctl import threadpool_limits
-
     from oracle import cgdr_oracle as O
 
-    cores = len(os.sched_getaffinity(0))
-    hs = slice(0, sample_heads)
+    H, Hg = v.shape[2], q.shape[2]
+    r = H // Hg
     arr = lambda t: t.float().cpu().numpy()
-    qh, kh, vh, hh, gh = arr(q[:, :, hs]), arr(k[:, :, hs]), arr(v[:, :, hs]), arr(h[:, :, hs]), arr(g[:, :, hs])
-    times = []
-    with threadpool_limits(cores):
-        O.chunk_o(qh[:, :2048], kh[:, :2048], vh[:, :2048], hh[:, :32], g=gh[:, :2048])   # warm-up
-        for i in range(repeats):
-            t0 = time.perf_counter()
-            O.chunk_o(qh, kh, vh, hh, g=gh)
-            times.append(time.perf_counter() - t0)
-            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
-    t = statistics.median(times)
-    frac = sample_heads / v.shape[2]
-    return dict(value=q.shape[0] * q.shape[1] * frac / t, unit="tokens/s", cores=cores, kind="port",
-                sample=f"numpy oracle chunk_o (exact fp32), B=1 T={q.shape[1]} on {sample_heads} of "
-                       f"{v.shape[2]} heads, median of {repeats}; value scaled to all heads ({t:.2f} s per run)")
+    qh, kh = arr(q[:, :, : max(1, sample_heads // r)]), arr(k[:, :, : max(1, sample_heads // r)])
+    vh, hh, gh = arr(v[:, :, :sample_heads]), arr(h[:, :, :sample_heads]), arr(g[:, :, :sample_heads])
+    run = lambda lo, hi, t: O.chunk_o(qh[:, :t, lo // r:hi // r], kh[:, :t, lo // r:hi // r], vh[:, :t, lo:hi],
+                                      hh[:, :(t + 63) // 64, lo:hi], g=gh[:, :t, lo:hi])
+    res = head_parallel_cpu(run, sample_heads, r, q.shape[1], repeats, "numpy oracle chunk_o (exact fp32), B=1")
+    return cpu_report(res, q.shape[0] * q.shape[1], sample_heads / H)
 
 
 def progress(msg: str) -> None:
@@ -183,28 +213,17 @@ def make_wy_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
 
 
 def wy_cpu_baseline(torch, k, v, beta, a, sample_heads, repeats):
-    from threadpoolctl import threadpool_limits
-
     from oracle import cgdr_oracle as O
 
-    cores = len(os.sched_getaffinity(0))
-    hs = slice(0, sample_heads)
+    H, Hg = v.shape[2], k.shape[2]
+    r = H // Hg
     arr = lambda t: t.float().cpu().numpy()
-    kh, vh, bh, ah = arr(k[:, :, hs]), arr(v[:, :, hs]), arr(beta[:, :, hs]), arr(a[:, :, hs])
-    times = []
-    with threadpool_limits(cores):
-        O.wy_prepare(kh[:, :256], vh[:, :256], bh[:, :256], ah[:, :256])   # warm-up
-        for i in range(repeats):
-            t0 = time.perf_counter()
-            O.wy_prepare(kh, vh, bh, ah)
-            times.append(time.perf_counter() - t0)
-            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
-    t = statistics.median(times)
-    frac = sample_heads / v.shape[2]
-    return dict(value=k.shape[0] * k.shape[1] * frac / t, unit="tokens/s", cores=cores, kind="port",
-                sample=f"numpy oracle wy_prepare (float64, one solve per chunk and head), B=1 T={k.shape[1]} "
-                       f"on {sample_heads} of {v.shape[2]} heads, median of {repeats}; value scaled to all heads "
-                       f"({t:.2f} s per run)")
+    kh = arr(k[:, :, : max(1, sample_heads // r)])
+    vh, bh, ah = arr(v[:, :, :sample_heads]), arr(beta[:, :, :sample_heads]), arr(a[:, :, :sample_heads])
+    run = lambda lo, hi, t: O.wy_prepare(kh[:, :t, lo // r:hi // r], vh[:, :t, lo:hi], bh[:, :t, lo:hi], ah[:, :t, lo:hi])
+    res = head_parallel_cpu(run, sample_heads, r, k.shape[1], repeats,
+                            "numpy oracle wy_prepare (float64, one solve per chunk and head), B=1")
+    return cpu_report(res, k.shape[0] * k.shape[1], sample_heads / H)
 
 
 def main_wy(args, torch, cgdr_amd, dev, forward: bool):
@@ -255,7 +274,7 @@ def main_wy(args, torch, cgdr_amd, dev, forward: bool):
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "algorithmic_bytes": nbytes},
     }
     if not args.no_cpu_baseline and not forward:
-        out["cpu_baseline"] = wy_cpu_baseline(torch, k, v, beta, a, args.cpu_sample_heads or 8, args.cpu_repeats or 3)
+        out["cpu_baseline"] = wy_cpu_baseline(torch, k, v, beta, a, args.cpu_sample_heads or 16, args.cpu_repeats or 3)
         out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
 
@@ -303,7 +322,7 @@ def main_chunk_o(args, torch, cgdr_amd, dev):
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "algorithmic_bytes": nbytes},
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = chunk_o_cpu_baseline(torch, q, k, v, h, g, args.cpu_sample_heads or 8,
+        out["cpu_baseline"] = chunk_o_cpu_baseline(torch, q, k, v, h, g, args.cpu_sample_heads or 16,
                                                    args.cpu_repeats or 3)
         out["cpu_baseline"]["speedup"] = out["value"] / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)
