@@ -67,6 +67,58 @@ def make_inputs(torch, dev, B, T, H, Hg, K, V, seed=0):
     return k, w, u, g
 
 
+# FwdH workloads besides the headline prefill (each FwdH configuration at its own shape):
+# two bf16 sequences with h0; 16 packed sequences of seeded lengths in [64, 8192] (none a
+# multiple of 64) with per-sequence h0; wide value heads with a strongly decaying gate.
+FWD_H_WORKLOADS = {
+    "prefill": dict(desc="ChunkGatedDeltaRuleFwdH long-context prefill", B=1, T=32768, H=32, Hg=32, K=128,
+                    V=128, h0=False, shift=0.0),
+    "two_seq": dict(desc="ChunkGatedDeltaRuleFwdH two bf16 sequences with h0", B=2, T=2048, H=16, Hg=16,
+                    K=128, V=128, h0=True, shift=0.0),
+    "varlen": dict(desc="ChunkGatedDeltaRuleFwdH 16 packed sequences of lengths U[64,8192] with per-sequence h0",
+                   B=1, T=None, H=32, Hg=32, K=128, V=128, h0=True, shift=0.0, n_seq=16),
+    "wide_v": dict(desc="ChunkGatedDeltaRuleFwdH wide value heads, gate logsigmoid(randn-2)", B=4, T=8192, H=8,
+                   Hg=8, K=128, V=256, h0=True, shift=-2.0),
+}
+
+
+def make_workload_inputs(torch, dev, name: str, seed: int = 0):
+    """Synthetic inputs of one FwdH workload, resident on the device (the distributions of
+    make_inputs; g the chunk-local cumsum of logsigmoid(randn + shift), per sequence, stored
+    head-major; h0 = randn * 0.1 fp32).  Returns (tensors, sizes); cu_seqlens stays on the host."""
+    c = FWD_H_WORKLOADS[name]
+    B, H, Hg, K, V = c["B"], c["H"], c["Hg"], c["K"], c["V"]
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(seed)
+    cu = None
+    if c.get("n_seq"):
+        lens = torch.randint(64, 8193, (c["n_seq"],), generator=gen)
+        lens = torch.where(lens % 64 == 0, torch.where(lens < 8192, lens + 1, lens - 1), lens)
+        cu = torch.cat([torch.zeros(1, dtype=torch.int64), lens.cumsum(0)])
+        T = int(cu[-1])
+    else:
+        T = c["T"]
+        cu = None
+    bounds = [(int(cu[i]), int(cu[i + 1])) for i in range(len(cu) - 1)] if cu is not None else [(0, T)]
+    N = len(bounds) if cu is not None else B
+    NT = sum((e - s + 63) // 64 for s, e in bounds)
+    k = torch.nn.functional.normalize(torch.randn(B, T, Hg, K, generator=gen), dim=-1)
+    w = torch.randn(B, T, H, K, generator=gen) * K ** -0.5
+    u = torch.randn(B, T, H, V, generator=gen)
+    inc = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen) + c["shift"])
+    g = torch.empty_like(inc)
+    for s, e in bounds:          # chunk-local cumsum within each sequence
+        L = e - s
+        pad = (L + 63) // 64 * 64 - L
+        x = torch.nn.functional.pad(inc[:, s:e], (0, 0, 0, pad)).view(B, -1, 64, H).cumsum(dim=2)
+        g[:, s:e] = x.view(B, -1, H)[:, :L]
+    h0 = torch.randn(N, H, K, V, generator=gen) * 0.1 if c["h0"] else None
+    t = dict(k=k.to(dev, torch.bfloat16), w=w.to(dev, torch.bfloat16), u=u.to(dev, torch.bfloat16),
+             g=g.to(dev).transpose(1, 2).contiguous().transpose(1, 2),
+             initial_state=None if h0 is None else h0.to(dev), cu_seqlens=cu)
+    return t, dict(B=B, T=T, H=H, Hg=Hg, K=K, V=V, N=N, NT=NT, chunk_size=64)
+
+
 def head_parallel_cpu(run, n_heads: int, group: int, T: int, repeats: int, what: str):
     """Time an oracle over heads [0, n_heads) of T tokens on the host's cores.
 
@@ -352,6 +404,10 @@ def main():
     ap.add_argument("--op", choices=("fwd_h", "chunk_o", "wy", "forward"), default="fwd_h",
                     help="fwd_h: the headline FwdH step (default); chunk_o: the chunk output; wy: the WY "
                          "producer; forward: WY -> FwdH -> chunk output")
+    ap.add_argument("--workload", choices=tuple(FWD_H_WORKLOADS), default="prefill",
+                    help="fwd_h shape: prefill (B=1 T=32768 H=32 K=V=128, the default), two_seq (B=2 T=2048 "
+                         "H=16, h0), varlen (16 packed sequences of lengths U[64,8192], h0), wide_v (B=4 T=8192 "
+                         "H=8 K=128 V=256, strongly decaying gate, h0); the CPU baseline runs on prefill only")
     ap.add_argument("--numerics", choices=("default", "contest"), default="default",
                     help="fwd_h rounding model: default (the Triton kernel's) or contest (run()'s casts)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -382,15 +438,22 @@ def main():
         return main_chunk_o(args, torch, cgdr_amd, dev)
     if args.op in ("wy", "forward"):
         return main_wy(args, torch, cgdr_amd, dev, forward=args.op == "forward")
-    W = WORKLOAD
-    B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
-    NT = (T + 63) // 64
-    k, w, u, g = make_inputs(torch, dev, B, T, H, Hg, K, V)
+    if args.workload == "prefill":
+        W = WORKLOAD
+        B, T, H, Hg, K, V = W["B"], W["T"], W["H"], W["Hg"], W["K"], W["V"]
+        N, NT = B, (T + 63) // 64
+        k, w, u, g = make_inputs(torch, dev, B, T, H, Hg, K, V)
+        h0 = cu = None
+    else:
+        t_in, W = make_workload_inputs(torch, dev, args.workload)
+        B, T, H, Hg, K, V, N, NT = (W[x] for x in ("B", "T", "H", "Hg", "K", "V", "N", "NT"))
+        k, w, u, g, h0, cu = (t_in[x] for x in ("k", "w", "u", "g", "initial_state", "cu_seqlens"))
     torch.cuda.synchronize()
-    progress("fwd_h inputs resident in HBM")
+    progress(f"fwd_h inputs ({args.workload}) resident in HBM")
 
     def step():
-        return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, output_final_state=True, numerics=args.numerics)
+        return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, initial_state=h0, output_final_state=True,
+                                                     cu_seqlens=cu, numerics=args.numerics)
 
     for _ in range(args.warmup):
         step()
@@ -411,16 +474,16 @@ def main():
     avg_ms = sum(kern_ms) / len(kern_ms)
     progress(f"timed {args.steps} fwd_h steps")
 
-    nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, B)
+    nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, N, h0_bytes=4 if h0 is not None else 0)
     flops = algorithmic_flops(B, NT, H, K, V)
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = B * T * args.steps / wall
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
-    plan = cgdr_amd.plan(k, u, numerics=args.numerics)
+    plan = cgdr_amd.plan(k, u, cu_seqlens_len=None if cu is None else len(cu), numerics=args.numerics)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "cgdr_fwd_h_bf16_T32768_H32_hbm_traffic.md")
-    if os.path.exists(tfile):
+    if os.path.exists(tfile) and args.workload == "prefill" and args.numerics == "default":
         for line in open(tfile):
             if line.startswith("traffic_bytes_per_launch:"):
                 traffic = int(line.split(":")[1])
@@ -438,9 +501,9 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "ChunkGatedDeltaRuleFwdH long-context prefill", **W,
-                   "h0": None, "output_final_state": True, "numerics": args.numerics,
-                   "parallelism": "none (1 GPU)"},
+        "config": {"workload": FWD_H_WORKLOADS[args.workload]["desc"], **W,
+                   "h0": "fp32 [N,H,K,V]" if h0 is not None else None, "output_final_state": True,
+                   "numerics": args.numerics, "parallelism": "none (1 GPU)"},
         "hbm_gbps": achieved,
         "kernel_ms": avg_ms,
         "kernel_ms_min": min(kern_ms),
@@ -451,7 +514,7 @@ def main():
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "algorithmic_bytes": nbytes},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload == "prefill":
         out["cpu_baseline"] = cpu_baseline(torch, k, w, u, g, args.cpu_sample_heads or 32, args.cpu_repeats or 7)
         out["cpu_baseline"]["speedup"] = tokens_per_s / out["cpu_baseline"]["value"]
     print(json.dumps(out), flush=True)

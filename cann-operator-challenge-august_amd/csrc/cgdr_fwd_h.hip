@@ -168,6 +168,11 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     // Enough workgroups to cover the 256 CUs first, then wider V-tiles (fewer K/W re-reads).
     ncw = 1;
     if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
+    // The bf16 kernel runs one task workgroup per CU, and every task walks its whole sequence:
+    // when 16-column tiles would need more than one round of the chip, 32-column tiles need
+    // half the rounds.  Measured at B=4, T=8192, H=8, K=128, V=256 (512 vs 256 tasks): 297 us
+    // with 16 columns, 198 us with 32.
+    if (a->in_dtype == CGDR_BF16 && V % 32 == 0 && pairs * (V / 16) > kCUs) ncw = 2;
   }
   if (V % (16 * ncw) != 0) ncw = 1;
   if (a->in_dtype == CGDR_F32) {

@@ -285,6 +285,31 @@ __device__ __forceinline__ Task decode_task(const FwdHParams& p, int task_id) {
   return t;
 }
 
+// Dispatch order of a packed variable-length batch.  Task ids are sequence-major
+// ((n * H + head) * n_vtiles + vtile), and xcd_remap hands every XCD a contiguous range of
+// dispatch indices, so in that order an XCD would receive whole sequences and the XCD with
+// the longest ones would set the kernel's time.  With cu_seqlens and H % 8 == 0 a dispatch
+// index is read instead as (XCD block, sequence rank, head within the block, V-tile): every
+// XCD gets H/8 heads of every sequence (equal work), a head's V-tiles and the heads sharing
+// a key head stay on one XCD, and within an XCD longer sequences are dispatched first
+// (ranked by length, longest first, ties by index, when N <= 64; natural order above that).
+// Fixed-length batches keep the identity order.  Every lane of the calling wave must be active.
+__device__ __forceinline__ int order_task(const FwdHParams& p, int d) {
+  if (p.cu_seqlens == nullptr || (p.H & 7) != 0) return d;
+  const int N = (int)p.N;
+  const sched::VarlenSlot s = sched::varlen_slot(d, p.n_tasks, (int)p.H, p.n_vtiles);
+  int n = s.rank;
+  if (N <= 64) {
+    // lane m < N holds sequence m's rank; they are a permutation of 0 .. N-1, so exactly one
+    // lane matches
+    const int lane = threadIdx.x & 63;
+    const int rank = lane < N ? sched::seq_rank(p.cu_seqlens, N, lane) : -1;
+    const unsigned long long hit = __ballot(rank == s.rank);
+    if (hit != 0ull) n = __ffsll(hit) - 1;
+  }
+  return (n * (int)p.H + s.head) * p.n_vtiles + s.vtile;
+}
+
 // =============================================================================================
 // bf16 pipeline kernel.
 //   KD      key dim (32, 64, 128, 256)
@@ -362,7 +387,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     task_id = x * m + (helper ? i - m : i);
   }
   if (task_id >= p.n_tasks) return;   // uniform per workgroup
-  const Task tk = decode_task(p, task_id);
+  const Task tk = decode_task(p, order_task(p, task_id));
   if constexpr (FULL)
     if (p.redo[(int64_t)tk.n * p.H + tk.head] == 0) return;   // uniform: the fast pass was exact
   const int NC = tk.nc;
@@ -1062,7 +1087,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int task_id = xcd_remap(blockIdx.x, gridDim.x);
   if (task_id >= p.n_tasks) return;
-  const Task tk = decode_task(p, task_id);
+  const Task tk = decode_task(p, order_task(p, task_id));
   const int vbase = tk.vtile * VT;
   const int hk = tk.head / p.head_ratio;
   const int g = lane >> 4, n = lane & 15;

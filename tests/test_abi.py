@@ -212,9 +212,13 @@ def test_plan_headline_fills_the_chip(lib):
     p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128))
     assert p.kernel == 0 and p.v_tile == 32 and p.workgroups == 256
     assert p.lds_bytes <= 160 * 1024
-    # helpers need the doubled grid to fit the chip and tasks in multiples of 8 (per XCD)
+    # helpers need the doubled grid to fit the chip and tasks in multiples of 8 (per XCD);
+    # without them, 32-column tiles when 16-column ones would take more than one round of
+    # the chip at one task workgroup per CU
     p = _abi.get_plan(_args(B=2, T=4096, H=32, Hg=32, K=128, V=128))
-    assert p.v_tile == 16 and p.workgroups == 2 * 32 * 8
+    assert p.v_tile == 32 and p.workgroups == 2 * 32 * 4
+    p = _abi.get_plan(_args(B=1, T=4096, H=16, Hg=16, K=128, V=128))   # 128 tasks of 16 columns
+    assert p.v_tile == 32 and p.workgroups == 2 * 16 * 4                # helper mode
     p = _abi.get_plan(_args(B=1, T=4096, H=6, Hg=6, K=128, V=128))
     assert p.workgroups == 6 * 8
 
