@@ -191,7 +191,10 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     // With helper workgroups the task's loads are L2 hits and one load wave keeps up; at most
     // 8 waves per workgroup (two per SIMD), so that no wave is squeezed below 256 VGPRs.
     // K = 256: one load wave (two push the kernel past 256 VGPRs into scratch spills).
-    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = (use_helpers || K == 256) ? 1 : 2;
+    // 32-column tiles without helpers: one load wave (with the L2 touches 2 chunks ahead,
+    // below) measured 925 us against 1,020 us with two, for 16 packed sequences of lengths
+    // U[64, 8192] at H=32, K=V=128.
+    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = (use_helpers || K == 256 || ncw == 2) ? 1 : 2;
     if (pl->kernel == 2 && nlw == 4) nlw = 2;   // contest instantiations: 1 or 2 load waves
     while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
     pl->nlw = nlw;
@@ -235,7 +238,9 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.h0_f32 = a->h0_dtype == CGDR_F32;
   p.final_f32 = a->final_dtype == CGDR_F32;
   p.has_g = a->g != nullptr;
-  p.prefetch = env_int("CGDR_FWD_H_PREFETCH", 4);
+  // L2 touch distance of store wave 0 without helpers: 2 chunks for 32-column tiles (one load
+  // wave; measured 925 us at 2, 937 at 3, 975 at 4 for the packed batch above), 4 for 16
+  p.prefetch = env_int("CGDR_FWD_H_PREFETCH", pl.ncw == 2 ? 2 : 4);
   p.helpers = pl.helpers;
   p.helper_lead = env_int("CGDR_FWD_H_HELPER_LEAD", 4);
   {
