@@ -120,8 +120,10 @@ def test_token_major_g_needs_head_major_workspace(lib):
     assert _status(_with_g(_args(B=1, T=256, H=3, Hg=1))) == (_abi.CGDR_OK, 3 * 256 * 4)
     assert _status(_with_g(_args(B=1, T=200, H=3, Hg=1))) == (_abi.CGDR_OK, 2560)
     assert _status(_with_g(_args(B=1, T=200, H=3, Hg=1), token_major=False)) == (_abi.CGDR_OK, 0)
-    # varlen, 2 sequences x 3 heads x 4 V-tiles = 24 tasks: helpers, 24 progress lines
-    assert _status(_with_g(_args(varlen=[0, 61, 64], T=64, H=3, Hg=1)))[1] == 3 * 64 * 4 + 24 * 128
+    # varlen, 2 sequences x 3 heads: one chunk per sequence, too short for helper workgroups
+    assert _status(_with_g(_args(varlen=[0, 61, 64], T=64, H=3, Hg=1)))[1] == 3 * 64 * 4
+    # 2 sequences of 96 and 100 chunks x 3 heads x 4 V-tiles = 24 tasks: helpers, 24 progress lines
+    assert _status(_with_g(_args(varlen=[0, 6144, 12544], T=12544, H=3, Hg=1)))[1] == 3 * 12544 * 4 + 24 * 128
 
 
 def test_contest_numerics_need_one_flag_per_head(lib):
@@ -131,6 +133,9 @@ def test_contest_numerics_need_one_flag_per_head(lib):
     a.numerics = _abi.CGDR_NUMERICS_CONTEST
     assert _status(a) == (_abi.CGDR_OK, 3 * 4)
     a = _args(varlen=[0, 61, 64], T=64, H=3, Hg=1)
+    a.numerics = _abi.CGDR_NUMERICS_CONTEST
+    assert _status(a)[1] == 2 * 3 * 4
+    a = _args(varlen=[0, 6144, 12544], T=12544, H=3, Hg=1)
     a.numerics = _abi.CGDR_NUMERICS_CONTEST
     assert _status(a)[1] == 24 * 128 + 2 * 3 * 4
 
@@ -217,18 +222,23 @@ def test_plan_headline_fills_the_chip(lib):
     # the chip at one task workgroup per CU
     p = _abi.get_plan(_args(B=2, T=4096, H=32, Hg=32, K=128, V=128))
     assert p.v_tile == 32 and p.workgroups == 2 * 32 * 4
-    p = _abi.get_plan(_args(B=1, T=4096, H=16, Hg=16, K=128, V=128))   # 128 tasks of 16 columns
+    p = _abi.get_plan(_args(B=1, T=8192, H=16, Hg=16, K=128, V=128))   # 128 tasks of 16 columns
     assert p.v_tile == 32 and p.workgroups == 2 * 16 * 4                # helper mode
-    p = _abi.get_plan(_args(B=1, T=4096, H=6, Hg=6, K=128, V=128))
+    p = _abi.get_plan(_args(B=1, T=8192, H=6, Hg=6, K=128, V=128))
     assert p.workgroups == 6 * 8
+    # sequences under 96 chunks: no helpers, 16-column tiles while they fit one round
+    p = _abi.get_plan(_args(B=1, T=4096, H=16, Hg=16, K=128, V=128))
+    assert p.v_tile == 16 and p.workgroups == 16 * 8
 
 
 def test_helper_mode_workspace_holds_progress_counters(lib):
     # one 128-byte progress line per task, after the (256-byte rounded) head-major g copy
-    a = _args(B=1, T=200, H=32, Hg=32, K=128, V=128)
+    # (helpers from 96 chunks per sequence on)
+    a = _args(B=1, T=6100, H=32, Hg=32, K=128, V=128)
     assert _status(a) == (_abi.CGDR_OK, 128 * 128)
-    a = _with_g(_args(B=1, T=200, H=32, Hg=32, K=128, V=128))
-    assert _status(a) == (_abi.CGDR_OK, ((32 * 200 * 4 + 255) // 256) * 256 + 128 * 128)
+    a = _with_g(_args(B=1, T=6100, H=32, Hg=32, K=128, V=128))
+    assert _status(a) == (_abi.CGDR_OK, ((32 * 6100 * 4 + 255) // 256) * 256 + 128 * 128)
+    assert _status(_args(B=1, T=6000, H=32, Hg=32, K=128, V=128)) == (_abi.CGDR_OK, 0)   # 94 chunks
 
 
 def test_wrapper_refuses_cpu_tensors():

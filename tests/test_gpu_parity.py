@@ -207,9 +207,10 @@ def test_helper_workgroups_change_nothing(dev, lens):
         inp = _case(62, 1, int(cu[-1]), 4, 128, 128, shift=4.0, cu=cu, profile="wy")
     d = dev_inputs(inp, torch.bfloat16, dev)
     base = _with_env("CGDR_FWD_H_HELPERS", 0, lambda: _with_env("CGDR_FWD_H_VTILE", 32, lambda: abi_call(d)))
+    # helpers forced on (these sequences are shorter than the default's helper threshold)
     for key, val in (("CGDR_FWD_H_HELPERS", 1), ("CGDR_FWD_H_HELPER_LEAD", 0),
                      ("CGDR_FWD_H_HELPER_LEAD", 100000), ("CGDR_FWD_H_HELPER_WAVES", 1)):
-        out = _with_env(key, val, lambda: abi_call(d))
+        out = _with_env("CGDR_FWD_H_HELPERS", 1, lambda: _with_env(key, val, lambda: abi_call(d)))
         for a, b in zip(base, out):
             assert torch.equal(a, b), (key, val)
 
