@@ -410,6 +410,9 @@ def main():
                          "H=8 K=128 V=256, strongly decaying gate, h0); the CPU baseline runs on prefill only")
     ap.add_argument("--numerics", choices=("default", "contest"), default="default",
                     help="fwd_h rounding model: default (the Triton kernel's) or contest (run()'s casts)")
+    ap.add_argument("--tuning", default=None,
+                    help="fwd_h launch-plan overrides as JSON (fields of cgdr_fwd_h_tuning, e.g. "
+                         "'{\"load_waves\": 2}'); outputs do not depend on them")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB fp32 elementwise copy (the reference kernel of known "
                          "HBM traffic that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -451,9 +454,11 @@ def main():
     torch.cuda.synchronize()
     progress(f"fwd_h inputs ({args.workload}) resident in HBM")
 
+    tuning = json.loads(args.tuning) if args.tuning else None
+
     def step():
         return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, initial_state=h0, output_final_state=True,
-                                                     cu_seqlens=cu, numerics=args.numerics)
+                                                     cu_seqlens=cu, numerics=args.numerics, tuning=tuning)
 
     for _ in range(args.warmup):
         step()
@@ -472,14 +477,15 @@ def main():
     wall = time.perf_counter() - t0
     kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     avg_ms = sum(kern_ms) / len(kern_ms)
-    progress(f"timed {args.steps} fwd_h steps")
+    progress(f"timed {args.steps} fwd_h steps; per-step ms: " + " ".join(f"{x:.4f}" for x in kern_ms))
 
     nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, N, h0_bytes=4 if h0 is not None else 0)
     flops = algorithmic_flops(B, NT, H, K, V)
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = B * T * args.steps / wall
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
-    plan = cgdr_amd.plan(k, u, cu_seqlens_len=None if cu is None else len(cu), numerics=args.numerics)
+    plan = cgdr_amd.plan(k, u, cu_seqlens_len=None if cu is None else len(cu), numerics=args.numerics, NT=NT,
+                         tuning=tuning)
 
     traffic = None
     tfile = os.path.join(ROOT, "profiles", "cgdr_fwd_h_bf16_T32768_H32_hbm_traffic.md")
@@ -503,7 +509,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": FWD_H_WORKLOADS[args.workload]["desc"], **W,
                    "h0": "fp32 [N,H,K,V]" if h0 is not None else None, "output_final_state": True,
-                   "numerics": args.numerics, "parallelism": "none (1 GPU)"},
+                   "numerics": args.numerics, "parallelism": "none (1 GPU)",
+                   **({"tuning": tuning} if tuning else {})},
         "hbm_gbps": achieved,
         "kernel_ms": avg_ms,
         "kernel_ms_min": min(kern_ms),

@@ -12,7 +12,7 @@ import ctypes
 import os
 
 CHUNK_SIZE = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CGDR_OK = 0
 CGDR_ERR_NULLPTR = 1
@@ -45,6 +45,33 @@ LIB_DIR = os.path.join(_PKG_ROOT, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libcgdr_fwd_h.so")
 
 _c_i64_p = ctypes.POINTER(ctypes.c_int64)
+
+
+class FwdHTuning(ctypes.Structure):
+    """Mirror of ``cgdr_fwd_h_tuning`` (launch-plan overrides; results never depend on them)."""
+
+    _fields_ = [
+        ("v_tile", ctypes.c_int32),
+        ("helpers", ctypes.c_int32),
+        ("load_waves", ctypes.c_int32),
+        ("stages", ctypes.c_int32),
+        ("prefetch", ctypes.c_int32),
+        ("helper_lead", ctypes.c_int32),
+        ("helper_waves", ctypes.c_int32),
+        ("cu_count", ctypes.c_int32),
+        ("xcd_count", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+def make_tuning(**kw) -> FwdHTuning:
+    """A ``cgdr_fwd_h_tuning`` with the library's choice everywhere except the given fields."""
+    t = FwdHTuning(helpers=-1, prefetch=-1, helper_lead=-1)
+    for k, v in kw.items():
+        if k not in dict(FwdHTuning._fields_):
+            raise ValueError(f"unknown tuning field {k!r}")
+        setattr(t, k, int(v))
+    return t
 
 
 class FwdHArgs(ctypes.Structure):
@@ -82,6 +109,7 @@ class FwdHArgs(ctypes.Structure):
         ("stride_v", ctypes.c_int64 * 3),
         ("stride_h0", ctypes.c_int64 * 2),
         ("stride_final", ctypes.c_int64 * 2),
+        ("tuning", ctypes.POINTER(FwdHTuning)),
     ]
 
 
@@ -96,6 +124,10 @@ class FwdHPlan(ctypes.Structure):
         ("stages", ctypes.c_int32),
         ("lds_bytes", ctypes.c_int32),
         ("workgroups", ctypes.c_int64),
+        ("helpers", ctypes.c_int32),
+        ("load_waves", ctypes.c_int32),
+        ("cu_count", ctypes.c_int32),
+        ("xcd_count", ctypes.c_int32),
     ]
 
 

@@ -34,10 +34,11 @@ HIP_FLAGS = [
     "-Wno-inline-asm",
 ]
 
-SOURCES = [os.path.join(CSRC, n) for n in ("cgdr_fwd_h.hip", "cgdr_chunk_o.hip", "cgdr_wy.hip")]
+SOURCES = [os.path.join(CSRC, n) for n in ("cgdr_fwd_h_k128.hip", "cgdr_fwd_h_k64.hip", "cgdr_fwd_h_k256.hip",
+                                           "cgdr_fwd_h_k32.hip", "cgdr_fwd_h.hip", "cgdr_chunk_o.hip", "cgdr_wy.hip")]
 RUNNER_SOURCE = os.path.join(CSRC, "cgdr_golden_runner.cpp")
-HEADERS = [os.path.join(CSRC, n) for n in ("cgdr_kernels.h", "cgdr_schedule.h", "cgdr_host.h", "cgdr_chunk_common.h",
-                                             "cgdr_chunk_o_kernel.h", "cgdr_wy_kernel.h")] + \
+HEADERS = [os.path.join(CSRC, n) for n in ("cgdr_kernels.h", "cgdr_fwd_h_dispatch.h", "cgdr_schedule.h", "cgdr_host.h",
+                                          "cgdr_chunk_common.h", "cgdr_chunk_o_kernel.h", "cgdr_wy_kernel.h")] + \
     [os.path.join(REPO_ROOT, "include", n) for n in ("cgdr_fwd_h.h", "cgdr_chunk_o.h", "cgdr_wy.h")]
 
 

@@ -20,6 +20,8 @@ Varlen metadata is validated on the host like ``prepare_chunk_indices`` in the r
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _abi
@@ -82,8 +84,11 @@ def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets,
 
 
 def _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT,
-            strides: dict, numerics: str = "default") -> None:
+            strides: dict, numerics: str = "default", tuning: dict | None = None) -> None:
     a = _abi.FwdHArgs()
+    if tuning:
+        t = _abi.make_tuning(**tuning)
+        a.tuning = ctypes.pointer(t)
     a.k, a.w, a.u = k.data_ptr(), w.data_ptr(), u.data_ptr()
     a.g = _ptr(g)
     a.initial_state = _ptr(h0)
@@ -143,9 +148,12 @@ def chunk_gated_delta_rule_fwd_h(
     chunk_offsets: torch.Tensor | None = None,
     final_state_dtype: torch.dtype = torch.float32,
     numerics: str = "default",
+    tuning: dict | None = None,
 ):
     """``(h, v_new, final_state)`` for token-major inputs; see the module docstring.
     ``numerics="contest"`` selects the contest reference's rounding model (bf16 inputs).
+    ``tuning`` overrides fields of the launch plan (``cgdr_fwd_h_tuning``: v_tile, helpers,
+    load_waves, stages, ...); outputs do not depend on it.
 
     ``g`` and ``initial_state`` may be any floating dtype; g is used in fp32 and
     initial_state in fp32 or bf16 (other dtypes are upcast to fp32).
@@ -196,7 +204,8 @@ def chunk_gated_delta_rule_fwd_h(
         stride_h0=h0.stride()[:2] if h0 is not None else None,
         stride_final=final.stride()[:2] if final is not None else None,
     )
-    _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT, strides, numerics)
+    _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT, strides, numerics,
+            tuning)
     return h, v_new, final
 
 
@@ -252,8 +261,10 @@ def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_S
 
 
 def plan(k: torch.Tensor, u: torch.Tensor, H: int | None = None, N: int | None = None,
-         cu_seqlens_len: int | None = None, numerics: str = "default") -> dict:
-    """Launch plan the library picks for token-major inputs of these shapes (host only)."""
+         cu_seqlens_len: int | None = None, numerics: str = "default", NT: int | None = None,
+         tuning: dict | None = None) -> dict:
+    """Launch plan the library picks for token-major inputs of these shapes (host only).
+    ``NT`` is the real chunk count of a packed batch (default ceil(T/64), a lower bound)."""
     B, T, Hg, K = k.shape
     H = u.shape[-2] if H is None else H
     V = u.shape[-1]
@@ -262,7 +273,10 @@ def plan(k: torch.Tensor, u: torch.Tensor, H: int | None = None, N: int | None =
     a.k = a.w = a.u = a.h = fake
     a.B, a.T, a.H, a.Hg, a.K, a.V = B, T, H, Hg, K, V
     a.N = B if N is None else N
-    a.NT = (T + CHUNK_SIZE - 1) // CHUNK_SIZE
+    a.NT = (T + CHUNK_SIZE - 1) // CHUNK_SIZE if NT is None else NT
+    if tuning:
+        t = _abi.make_tuning(**tuning)
+        a.tuning = ctypes.pointer(t)
     if cu_seqlens_len is not None:
         a.cu_seqlens = fake
         a.N = cu_seqlens_len - 1

@@ -26,8 +26,6 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // V-tile: 128 value columns when V allows it (and K <= 128, which keeps the LDS of one
 // workgroup at 48 KiB so three fit a CU), else 64, else 32.
 int pick_vtile(const cgdr_chunk_o_args* a) {
-  const int forced = cgdr_host::env_int("CGDR_CHUNK_O_VTILE", 0);
-  if ((forced == 32 || forced == 64 || (forced == 128 && a->K <= 128)) && a->V % forced == 0) return forced;
   if (a->V % 128 == 0 && a->K <= 128) return 128;
   if (a->V % 64 == 0) return 64;
   if (a->V % 32 == 0) return 32;
@@ -113,6 +111,7 @@ cgdr::ChunkOParams to_params(const cgdr_chunk_o_args* a, int vt) {
   p.T = a->T; p.NT = a->NT; p.V = a->V;
   p.H = (int32_t)a->H; p.Hg = (int32_t)a->Hg; p.N = (int32_t)a->N; p.n_vtiles = (int32_t)(a->V / vt);
   p.scale = a->scale;
+  p.n_xcd = cgdr_host::device_xcds();
   p.sq_b = a->stride_q[0]; p.sq_t = a->stride_q[1]; p.sq_h = a->stride_q[2];
   p.sk_b = a->stride_k[0]; p.sk_t = a->stride_k[1]; p.sk_h = a->stride_k[2];
   p.sv_b = a->stride_v[0]; p.sv_t = a->stride_v[1]; p.sv_h = a->stride_v[2];

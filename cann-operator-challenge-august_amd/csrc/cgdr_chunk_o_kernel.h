@@ -42,7 +42,7 @@ struct ChunkOParams {
   int64_t T, NT, V;
   int32_t H, Hg, N, n_vtiles;
   float scale;
-  int32_t reserved;
+  int32_t n_xcd;       // XCDs workgroups are dealt to round-robin
   int64_t sq_b, sq_t, sq_h;
   int64_t sk_b, sk_t, sk_h;
   int64_t sv_b, sv_t, sv_h;
@@ -78,7 +78,7 @@ __global__ void __launch_bounds__(256) cgdr_chunk_o_bf16_kernel(const ChunkOPara
 
   // unit -> (b, chunk, head, vtile); consecutive units share an XCD (V-tiles and the heads of
   // one key head reuse q and k from that XCD's L2)
-  int64_t unit = xcd_remap(blockIdx.x, gridDim.x);
+  int64_t unit = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
   const int vtile = (int)(unit % p.n_vtiles);
   unit /= p.n_vtiles;
   const int head = (int)(unit % p.H);

@@ -3,7 +3,8 @@
 // Host side: argument validation (the role of InferShapeChunkGatedDeltaRuleFwdH,
 // code/op_host/chunk_gated_delta_rule_fwd_h_infershape.cpp:135-298 of the reference, without
 // its Ascend-only limits B=1, K==V and N<=4), the launch plan (the role of the tiling function,
-// code/op_host/chunk_gated_delta_rule_fwd_h_tiling.cpp:152-261) and the kernel launch.
+// code/op_host/chunk_gated_delta_rule_fwd_h_tiling.cpp:152-261) and the kernel launch.  The
+// kernels of each key dimension are instantiated in cgdr_fwd_h_k{32,64,128,256}.hip.
 #include "../../include/cgdr_fwd_h.h"
 
 #include <hip/hip_runtime.h>
@@ -13,30 +14,21 @@
 #include <cstdlib>
 #include <cstring>
 
+#include "cgdr_fwd_h_dispatch.h"
 #include "cgdr_host.h"
 #include "cgdr_kernels.h"
 
 namespace {
 
-using cgdr_host::env_int;
+using cgdr_fwd::Plan;
 using cgdr_host::fail;
 
 constexpr int64_t kMaxHeadDim = 256;     // docs/problem.txt:466 (Triton wrapper assert K <= 256)
 constexpr int64_t kMaxValueDim = 1024;   // V-tiling lifts the reference's K == V <= 256
 constexpr int64_t kMaxTasks = 1 << 30;
-constexpr int64_t kCUs = 256;            // MI355X compute units (one workgroup per CU)
+constexpr int kDefaultCUs = 256;         // MI355X, when no device can be queried
+constexpr int kDefaultXCDs = 8;
 constexpr int64_t kHelperMinChunks = 96;  // shorter sequences run faster without helper workgroups
-
-struct Plan {
-  int kernel;        // 0 bf16 pipeline, 1 fp32
-  int helpers;       // bf16: one L2-prefetch workgroup per task
-  int ncw;           // compute waves (Vt = 16 * ncw)
-  int nlw;           // load waves (bf16 pipeline)
-  int stages;
-  int threads;
-  int lds;
-  int64_t tasks;
-};
 
 // Shape, stride and pointer checks shared by every entry point.
 cgdr_status validate(const cgdr_fwd_h_args* a) {
@@ -118,11 +110,47 @@ int bf16_max_stages(int64_t K, int ncw, int nlw);
 
 bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
 
+// Compute units and XCDs of the calling thread's current device (tuning overrides first; the
+// MI355X figures when no device answers, e.g. when planning on a host without a GPU).
+void topology(const cgdr_fwd_h_tuning* tu, int* cus, int* xcds) {
+  *cus = kDefaultCUs;
+  *xcds = kDefaultXCDs;
+  int dev = 0, v = 0;
+  const bool have_dev = hipGetDevice(&dev) == hipSuccess;
+  if (tu != nullptr && tu->cu_count > 0) *cus = tu->cu_count;
+  else if (have_dev && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+    *cus = v;
+  if (tu != nullptr && tu->xcd_count > 0) *xcds = tu->xcd_count;
+  else if (have_dev && hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0)
+    *xcds = v;
+  (void)hipGetLastError();   // a failed query on a host without a GPU is not the caller's error
+}
+
+cgdr_status check_tuning(const cgdr_fwd_h_tuning* tu) {
+  if (tu == nullptr) return CGDR_OK;
+  if (tu->v_tile != 0 && tu->v_tile != 16 && tu->v_tile != 32 && tu->v_tile != 64)
+    return fail(CGDR_ERR_INVALID, "tuning.v_tile must be 0, 16, 32 or 64, got %d", tu->v_tile);
+  if (tu->helpers < -1 || tu->helpers > 1) return fail(CGDR_ERR_INVALID, "tuning.helpers must be -1, 0 or 1");
+  if (tu->load_waves != 0 && tu->load_waves != 1 && tu->load_waves != 2 && tu->load_waves != 4)
+    return fail(CGDR_ERR_INVALID, "tuning.load_waves must be 0, 1, 2 or 4, got %d", tu->load_waves);
+  if (tu->stages != 0 && (tu->stages < 2 || tu->stages > 4))
+    return fail(CGDR_ERR_INVALID, "tuning.stages must be 0, 2, 3 or 4, got %d", tu->stages);
+  if (tu->prefetch < -1 || tu->prefetch > 64) return fail(CGDR_ERR_INVALID, "tuning.prefetch must be in [-1, 64]");
+  if (tu->helper_lead < -1) return fail(CGDR_ERR_INVALID, "tuning.helper_lead must be >= -1");
+  if (tu->helper_waves < 0 || tu->helper_waves > 16) return fail(CGDR_ERR_INVALID, "tuning.helper_waves must be in [0, 16]");
+  if (tu->cu_count < 0 || tu->xcd_count < 0) return fail(CGDR_ERR_INVALID, "tuning.cu_count/xcd_count must be >= 0");
+  if (tu->reserved != 0) return fail(CGDR_ERR_INVALID, "tuning.reserved must be 0");
+  return CGDR_OK;
+}
+
 // Kernel variant and grid.  The bf16 pipeline needs K in {32,64,128,256} (MFMA contraction
 // slices of 32 and the LDS swizzles), V a multiple of 16, 16-byte aligned rows of k/w/u
 // (direct-to-LDS loads move 16 bytes per lane) and 8-byte aligned rows of h/v_new.
 cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   cgdr_status st = validate(a);
+  if (st != CGDR_OK) return st;
+  const cgdr_fwd_h_tuning* tu = a->tuning;
+  st = check_tuning(tu);
   if (st != CGDR_OK) return st;
   const int64_t K = a->K, V = a->V;
   const int es = a->in_dtype == CGDR_BF16 ? 2 : 4;
@@ -152,32 +180,37 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
       return fail(CGDR_ERR_UNSUPPORTED, "h and v_new strides must be multiples of 8 bytes");
   }
 
+  int cus, xcds;
+  topology(tu, &cus, &xcds);
+  pl->cus = cus;
+  pl->xcds = xcds;
   int ncw;
   const int64_t pairs = a->N * a->H;
   // Helper mode (bf16 only): 32-column V-tiles, and one L2-prefetch workgroup beside every
-  // task, when tasks and helpers together fit the chip at one workgroup per CU.
-  const int helpers_env = env_int("CGDR_FWD_H_HELPERS", -1);
+  // task, when tasks and helpers together fit the device at one workgroup per CU (all
+  // resident at once) and the tasks split evenly over the XCDs.
+  const int helpers_req = tu != nullptr ? tu->helpers : -1;
   const bool helper_shape = a->in_dtype == CGDR_BF16 && K <= 128 && V % 32 == 0 &&
-                            (pairs * (V / 32)) % 8 == 0 && 2 * pairs * (V / 32) <= kCUs;
+                            (pairs * (V / 32)) % xcds == 0 && 2 * pairs * (V / 32) <= cus;
   // Helpers pay only on long sequences: at B=1, H=32, K=V=128 they measured 64.7 vs 54.7 us
   // (16-column tiles, no helpers) at 64 chunks per sequence and 112 vs 143 us at 128.  A packed
   // batch is judged by its mean sequence length.
   const int64_t seq_chunks = a->cu_seqlens != nullptr ? a->NT / (a->N > 0 ? a->N : 1) : a->NT;
-  const bool use_helpers = helper_shape && helpers_env != 0 && (helpers_env == 1 || seq_chunks >= kHelperMinChunks);
-  int forced = env_int("CGDR_FWD_H_VTILE", 0);
-  if (forced == 16 || forced == 32 || forced == 64) {
+  const bool use_helpers = helper_shape && helpers_req != 0 && (helpers_req == 1 || seq_chunks >= kHelperMinChunks);
+  const int forced = tu != nullptr ? tu->v_tile : 0;
+  if (forced != 0) {
     ncw = forced / 16;
   } else if (use_helpers) {
     ncw = 2;
   } else {
-    // Enough workgroups to cover the 256 CUs first, then wider V-tiles (fewer K/W re-reads).
+    // Enough workgroups to cover the CUs first, then wider V-tiles (fewer K/W re-reads).
     ncw = 1;
-    if (pairs * (V / 32) >= 512 && V % 32 == 0) ncw = 2;
+    if (pairs * (V / 32) >= 2 * cus && V % 32 == 0) ncw = 2;
     // The bf16 kernel runs one task workgroup per CU, and every task walks its whole sequence:
-    // when 16-column tiles would need more than one round of the chip, 32-column tiles need
+    // when 16-column tiles would need more than one round of the device, 32-column tiles need
     // half the rounds.  Measured at B=4, T=8192, H=8, K=128, V=256 (512 vs 256 tasks): 297 us
     // with 16 columns, 198 us with 32.
-    if (a->in_dtype == CGDR_BF16 && V % 32 == 0 && pairs * (V / 16) > kCUs) ncw = 2;
+    if (a->in_dtype == CGDR_BF16 && V % 32 == 0 && pairs * (V / 16) > cus) ncw = 2;
   }
   if (V % (16 * ncw) != 0) ncw = 1;
   if (a->in_dtype == CGDR_F32) {
@@ -186,38 +219,37 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     pl->nlw = 0;
     pl->stages = 1;
     pl->threads = 64 * ncw;
-    pl->lds = 0;
   } else {
     // bf16: the pipelined kernel, with the contest rounding model when asked for
     pl->kernel = a->numerics == CGDR_NUMERICS_CONTEST ? 2 : 0;
     if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
-    int nlw = env_int("CGDR_FWD_H_LOADERS", 0);
+    int nlw = tu != nullptr ? tu->load_waves : 0;
     // With helper workgroups the task's loads are L2 hits and one load wave keeps up; at most
     // 8 waves per workgroup (two per SIMD), so that no wave is squeezed below 256 VGPRs.
     // K = 256: one load wave (two push the kernel past 256 VGPRs into scratch spills).
     // 32-column tiles without helpers: one load wave (with the L2 touches 2 chunks ahead,
     // below) measured 925 us against 1,020 us with two, for 16 packed sequences of lengths
     // U[64, 8192] at H=32, K=V=128.
-    if (nlw != 1 && nlw != 2 && nlw != 4) nlw = (use_helpers || K == 256 || ncw == 2) ? 1 : 2;
+    if (nlw == 0) nlw = (use_helpers || K == 256 || ncw == 2) ? 1 : 2;
     if (pl->kernel == 2 && nlw == 4) nlw = 2;   // contest instantiations: 1 or 2 load waves
+    if (K == 256) nlw = 1;
     while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
     pl->nlw = nlw;
-    int stages = env_int("CGDR_FWD_H_STAGES", 0);
+    int stages = tu != nullptr ? tu->stages : 0;
     // deepest ring that fits the LDS and the vmcnt range
     const int max_stages = bf16_max_stages(K, ncw, nlw);
     if (stages < 2 || stages > max_stages) stages = max_stages;
     pl->stages = stages;
     pl->threads = 64 * (ncw + nlw + ncw + 1);   // compute, load, store (one per compute), gate
-    pl->lds = 0;
   }
   pl->tasks = a->N * a->H * (V / (16 * ncw));
   if (pl->tasks > kMaxTasks) return fail(CGDR_ERR_UNSUPPORTED, "too many tasks (%lld)", (long long)pl->tasks);
   // Helper workgroups (one per task, on the task's XCD) when the doubled grid still fits the
-  // chip at one workgroup per CU, so that tasks and helpers are all resident together.
+  // device at one workgroup per CU, so that tasks and helpers are all resident together.
   pl->helpers = 0;
-  if (pl->kernel != 1 && pl->tasks % 8 == 0 && 2 * pl->tasks <= kCUs && helpers_env != 0 &&
-      (use_helpers || helpers_env == 1))
+  if (pl->kernel != 1 && pl->tasks % xcds == 0 && 2 * pl->tasks <= cus && helpers_req != 0 &&
+      (use_helpers || helpers_req == 1))
     pl->helpers = 1;
   return CGDR_OK;
 }
@@ -243,77 +275,20 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.h0_f32 = a->h0_dtype == CGDR_F32;
   p.final_f32 = a->final_dtype == CGDR_F32;
   p.has_g = a->g != nullptr;
+  const cgdr_fwd_h_tuning* tu = a->tuning;
   // L2 touch distance of store wave 0 without helpers: 2 chunks for 32-column tiles (one load
   // wave; measured 925 us at 2, 937 at 3, 975 at 4 for the packed batch above), 4 for 16
-  p.prefetch = env_int("CGDR_FWD_H_PREFETCH", pl.ncw == 2 ? 2 : 4);
+  p.prefetch = (tu != nullptr && tu->prefetch >= 0) ? tu->prefetch : (pl.ncw == 2 ? 2 : 4);
   p.helpers = pl.helpers;
-  p.helper_lead = env_int("CGDR_FWD_H_HELPER_LEAD", 4);
+  p.helper_lead = (tu != nullptr && tu->helper_lead >= 0) ? tu->helper_lead : 4;
   {
-    int hw = env_int("CGDR_FWD_H_HELPER_WAVES", 4);
+    const int hw = (tu != nullptr && tu->helper_waves > 0) ? tu->helper_waves : 4;
     const int max_hw = pl.threads / 64;
-    p.helper_waves = hw < 1 ? 1 : (hw > max_hw ? max_hw : hw);
+    p.helper_waves = hw > max_hw ? max_hw : hw;
   }
+  p.n_xcd = pl.xcds;
   p.progress = nullptr;
   return p;
-}
-
-template <int KD, int NCW, int NLW, int STAGES, int NUM>
-hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
-  using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
-  const unsigned grid = (unsigned)(p.helpers ? 2 * tasks : tasks);
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, NUM>), dim3(grid),
-                     dim3(L::THREADS), 0, stream, p);
-  return hipGetLastError();
-}
-
-template <int KD, int NCW>
-hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
-  using L = cgdr::F32Layout<KD, NCW>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream, p);
-  return hipGetLastError();
-}
-
-// NUM: the kernel's numerics mode (0 default, 1 contest fast pass, 2 contest full pass)
-template <int KD, int NCW, int NLW, int NUM>
-hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4>())
-    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, NUM>(p, pl.tasks, s);
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3>())
-    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, NUM>(p, pl.tasks, s);
-  return launch_bf16<KD, NCW, NLW, 2, NUM>(p, pl.tasks, s);
-}
-
-template <int KD, int NCW, int NUM>
-hipError_t dispatch_bf16_nlw(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, NUM>(p, pl, s);
-  if constexpr (NUM == 0)
-    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, NUM>(p, pl, s);
-  return dispatch_bf16_stages<KD, NCW, 2, NUM>(p, pl, s);
-}
-
-template <int KD, int NUM>
-hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if constexpr (KD == 256) {
-    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
-  } else {
-    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, NUM>(p, pl, s);
-    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, NUM>(p, pl, s);
-    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
-  }
-}
-
-// Contest numerics: the fast pass (plain fp16 roundings) flags every (sequence, head) where a
-// saturating cast or nan_to_num could have changed a value; the full pass then recomputes just
-// those heads with the casts (its workgroups for unflagged heads return at once), without
-// helper workgroups, whose progress counters the fast pass has used up.
-template <int KD>
-hipError_t dispatch_contest(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  hipError_t e = dispatch_bf16<KD, 1>(p, pl, s);
-  if (e != hipSuccess) return e;
-  cgdr::FwdHParams q = p;
-  q.helpers = 0;
-  q.progress = nullptr;
-  return dispatch_bf16<KD, 2>(q, pl, s);
 }
 
 // Compile-time layout facts of the bf16 kernel instantiation a plan selects.
@@ -355,13 +330,6 @@ int bf16_max_stages(int64_t K, int ncw, int nlw) {
     case 128: return pick(std::integral_constant<int, 128>{});
     default: return pick(std::integral_constant<int, 256>{});
   }
-}
-
-template <int KD>
-hipError_t dispatch_f32(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
-  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
-  return launch_f32<KD, 1>(p, pl.tasks, s);
 }
 
 int lds_bytes_of(const Plan& pl, int64_t K) {
@@ -451,6 +419,10 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
   plan->stages = pl.stages;
   plan->lds_bytes = lds_bytes_of(pl, args->K);
   plan->workgroups = pl.helpers ? 2 * pl.tasks : pl.tasks;
+  plan->helpers = pl.helpers;
+  plan->load_waves = pl.nlw;
+  plan->cu_count = pl.cus;
+  plan->xcd_count = pl.xcds;
   return CGDR_OK;
 }
 
@@ -486,26 +458,11 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     e = hipGetLastError();
     if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "counter reset launch failed: %s", hipGetErrorString(e));
   }
-  if (pl.kernel == 0) {
-    switch (args->K) {
-      case 32: e = dispatch_bf16<32, 0>(p, pl, s); break;
-      case 64: e = dispatch_bf16<64, 0>(p, pl, s); break;
-      case 128: e = dispatch_bf16<128, 0>(p, pl, s); break;
-      default: e = dispatch_bf16<256, 0>(p, pl, s); break;
-    }
-  } else if (pl.kernel == 1) {
-    switch (args->K) {
-      case 32: e = dispatch_f32<32>(p, pl, s); break;
-      case 64: e = dispatch_f32<64>(p, pl, s); break;
-      default: e = dispatch_f32<128>(p, pl, s); break;
-    }
-  } else {
-    switch (args->K) {
-      case 32: e = dispatch_contest<32>(p, pl, s); break;
-      case 64: e = dispatch_contest<64>(p, pl, s); break;
-      case 128: e = dispatch_contest<128>(p, pl, s); break;
-      default: e = dispatch_contest<256>(p, pl, s); break;
-    }
+  switch (args->K) {
+    case 32: e = cgdr_fwd::launch_kd<32>(p, pl, s); break;
+    case 64: e = cgdr_fwd::launch_kd<64>(p, pl, s); break;
+    case 128: e = cgdr_fwd::launch_kd<128>(p, pl, s); break;
+    default: e = cgdr_fwd::launch_kd<256>(p, pl, s); break;
   }
   if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "kernel launch failed: %s", hipGetErrorString(e));
   return CGDR_OK;

@@ -1,11 +1,13 @@
 // cgdr_host.h -- host-side helpers shared by the operators of libcgdr_fwd_h: the
 // per-thread error message behind cgdr_last_error() (the role of OP_LOGE in the
-// reference's host code) and environment overrides used by tests and benchmarks.
+// reference's host code).
 #pragma once
 
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+
+#include <hip/hip_runtime.h>
 
 #include "../../include/cgdr_fwd_h.h"
 
@@ -21,10 +23,16 @@ inline cgdr_status fail(cgdr_status st, const char* fmt, ...) {
   return st;
 }
 
-inline int env_int(const char* name, int dflt) {
-  const char* s = getenv(name);
-  if (s == nullptr || *s == 0) return dflt;
-  return atoi(s);
+// XCDs of the calling thread's current device, which the hardware deals workgroups to
+// round-robin (8 on MI355X, the figure used when no device answers).
+inline int device_xcds() {
+  int dev = 0, v = 0;
+  int n = 8;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0)
+    n = v;
+  (void)hipGetLastError();
+  return n;
 }
 
 }  // namespace cgdr_host

@@ -103,7 +103,7 @@ struct FwdHParams {
   int32_t helpers;      // 1: one L2-prefetch workgroup per task (grid = 2 * n_tasks)
   int32_t helper_lead;  // chunks a helper runs ahead of its task's load waves
   int32_t helper_waves; // waves per helper workgroup issuing touches
-  int32_t reserved;
+  int32_t n_xcd;        // XCDs workgroups are dealt to round-robin (blockIdx % n_xcd)
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
                         // task (kProgressStride ints; zeroed before launch)
   int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
@@ -223,9 +223,9 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Task decoding shared by both kernels.  Workgroups are dealt to the 8 XCDs round-robin
-// (blockIdx % 8), so consecutive task ids are remapped onto one XCD: the V-tiles of a head,
-// and the heads sharing a key head, then share that XCD's L2 for their K and W reads.
+// Task decoding shared by both kernels.  Workgroups are dealt to the XCDs round-robin
+// (blockIdx % n_xcd), so consecutive task ids are remapped onto one XCD: the V-tiles of a
+// head, and the heads sharing a key head, then share that XCD's L2 for their K and W reads.
 // Compile-time loop: f(std::integral_constant<int, I>) for I in [I0, N).
 template <int I0, int N, class F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -242,9 +242,9 @@ struct Task {
   int nc;                  // chunks this task walks (clamped so every write stays in bounds)
 };
 
-__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
-  const int q = nblocks >> 3, r = nblocks & 7;
-  const int xcd = bid & 7, local = bid >> 3;
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks, int nx) {
+  const int q = nblocks / nx, r = nblocks - q * nx;
+  const int xcd = bid % nx, local = bid / nx;
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
 }
 
@@ -288,16 +288,17 @@ __device__ __forceinline__ Task decode_task(const FwdHParams& p, int task_id) {
 // Dispatch order of a packed variable-length batch.  Task ids are sequence-major
 // ((n * H + head) * n_vtiles + vtile), and xcd_remap hands every XCD a contiguous range of
 // dispatch indices, so in that order an XCD would receive whole sequences and the XCD with
-// the longest ones would set the kernel's time.  With cu_seqlens and H % 8 == 0 a dispatch
-// index is read instead as (XCD block, sequence rank, head within the block, V-tile): every
-// XCD gets H/8 heads of every sequence (equal work), a head's V-tiles and the heads sharing
-// a key head stay on one XCD, and within an XCD longer sequences are dispatched first
+// the longest ones would set the kernel's time.  With cu_seqlens and H % n_xcd == 0 a
+// dispatch index is read instead as (XCD block, sequence rank, head within the block,
+// V-tile): every XCD gets H/n_xcd heads of every sequence (equal work), a head's V-tiles and
+// the heads sharing a key head stay on one XCD, and within an XCD longer sequences are
+// dispatched first
 // (ranked by length, longest first, ties by index, when N <= 64; natural order above that).
 // Fixed-length batches keep the identity order.  Every lane of the calling wave must be active.
 __device__ __forceinline__ int order_task(const FwdHParams& p, int d) {
-  if (p.cu_seqlens == nullptr || (p.H & 7) != 0) return d;
+  if (p.cu_seqlens == nullptr || ((int)p.H % p.n_xcd) != 0) return d;
   const int N = (int)p.N;
-  const sched::VarlenSlot s = sched::varlen_slot(d, p.n_tasks, (int)p.H, p.n_vtiles);
+  const sched::VarlenSlot s = sched::varlen_slot(d, p.n_tasks, (int)p.H, p.n_vtiles, p.n_xcd);
   int n = s.rank;
   if (N <= 64) {
     // lane m < N holds sequence m's rank; they are a permutation of 0 .. N-1, so exactly one
@@ -375,13 +376,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
   const int lane = threadIdx.x & 63;
-  const int slot = xcd_remap(blockIdx.x, gridDim.x);
-  // With helpers the grid is 2 * n_tasks (n_tasks a multiple of 8): every XCD holds m tasks
-  // followed by their m helpers, so a helper and its task share that XCD's L2.
+  const int slot = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
+  // With helpers the grid is 2 * n_tasks (n_tasks a multiple of n_xcd): every XCD holds m
+  // tasks followed by their m helpers, so a helper and its task share that XCD's L2.
   int task_id = slot;
   bool helper = false;
   if (p.helpers) {
-    const int m = p.n_tasks >> 3;
+    const int m = p.n_tasks / p.n_xcd;
     const int x = slot / (2 * m), i = slot - x * 2 * m;
     helper = i >= m;
     task_id = x * m + (helper ? i - m : i);
@@ -511,6 +512,10 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     const int max_idle = 8 * NC + 4096;
     while (issued < NC) {
       const int done = poll_l2(prog_addr);
+      // Chunks below done + D are already in the task's own loads (a helper that starts late,
+      // e.g. on a device shared with other work, skips them instead of touching them again).
+      const int lo = done + D;
+      if (issued < lo) issued += (lo - issued + hwaves - 1) / hwaves * hwaves;
       int target = done + D + p.helper_lead;
       target = target < NC ? target : NC;
       if (issued < target) {
@@ -1085,7 +1090,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   float* Gs = smem + L::G_OFF / 4;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int task_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int task_id = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
   if (task_id >= p.n_tasks) return;
   const Task tk = decode_task(p, order_task(p, task_id));
   const int vbase = tk.vtile * VT;

@@ -24,16 +24,17 @@ constexpr int loop_allowance(int c, int D, int NC) { return (D >= 2 && c + D < N
 // outstanding, all full iff D-1 < NC-1.
 constexpr int prologue_allowance(int D, int NC) { return (D >= 2 && D < NC) ? D - 1 : 0; }
 
-// Dispatch order of a packed variable-length batch (cu_seqlens given, H % 8 == 0, so that
-// n_tasks = N * H * nv is a multiple of 8 and each XCD's range of dispatch indices holds
-// q = n_tasks / 8 of them).  Dispatch index d is read as (XCD block x, sequence rank r, head
-// within the block, V-tile): block x gets heads [x * H/8, (x+1) * H/8) of every sequence, and
-// within a block the rank varies slowest, so the longest sequences are dispatched first.
+// Dispatch order of a packed variable-length batch (cu_seqlens given, H % nx == 0 for nx XCDs,
+// so that n_tasks = N * H * nv is a multiple of nx and each XCD's range of dispatch indices
+// holds q = n_tasks / nx of them).  Dispatch index d is read as (XCD block x, sequence rank r,
+// head within the block, V-tile): block x gets heads [x * H/nx, (x+1) * H/nx) of every
+// sequence, and within a block the rank varies slowest, so the longest sequences are
+// dispatched first.
 struct VarlenSlot {
   int rank, head, vtile;
 };
-constexpr VarlenSlot varlen_slot(int d, int n_tasks, int H, int nv) {
-  const int hx = H >> 3, q = n_tasks >> 3;
+constexpr VarlenSlot varlen_slot(int d, int n_tasks, int H, int nv, int nx) {
+  const int hx = H / nx, q = n_tasks / nx;
   const int x = d / q, l = d - x * q;
   const int gi = l / nv;
   return VarlenSlot{gi / hx, x * hx + gi % hx, l % nv};

@@ -107,6 +107,7 @@ extern "C" cgdr_status cgdr_wy_launch(const cgdr_wy_args* a, void* stream) {
   p.w = a->w; p.u = a->u; p.gc = a->g_cumsum;
   p.T = a->T; p.NT = a->NT;
   p.H = (int32_t)a->H; p.Hg = (int32_t)a->Hg; p.N = (int32_t)a->N; p.beta_f32 = a->beta_dtype == CGDR_F32;
+  p.n_xcd = cgdr_host::device_xcds();
   p.sk_b = a->stride_k[0]; p.sk_t = a->stride_k[1]; p.sk_h = a->stride_k[2];
   p.sv_b = a->stride_v[0]; p.sv_t = a->stride_v[1]; p.sv_h = a->stride_v[2];
   p.sb_b = a->stride_beta[0]; p.sb_t = a->stride_beta[1]; p.sb_h = a->stride_beta[2];

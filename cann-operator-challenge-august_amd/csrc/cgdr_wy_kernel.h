@@ -48,6 +48,7 @@ struct WyParams {
   float* gc;
   int64_t T, NT;
   int32_t H, Hg, N, beta_f32;
+  int32_t n_xcd, reserved;   // XCDs workgroups are dealt to round-robin
   int64_t sk_b, sk_t, sk_h;
   int64_t sv_b, sv_t, sv_h;
   int64_t sb_b, sb_t, sb_h;
@@ -84,7 +85,7 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   const int e = n >> 2, qd = n & 3;
 
   // unit -> (b, chunk, head); consecutive units (the heads of one key head) share an XCD
-  int64_t unit = xcd_remap(blockIdx.x, gridDim.x);
+  int64_t unit = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
   const int head = (int)(unit % p.H);
   unit /= p.H;
   const int64_t chunk = unit % p.NT;

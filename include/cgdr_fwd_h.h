@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define CGDR_ABI_VERSION 1
+#define CGDR_ABI_VERSION 2
 #define CGDR_CHUNK_SIZE 64
 
 /* Status codes.  The reference's aclnnStatus values for the same conditions are
@@ -77,6 +77,25 @@ typedef enum cgdr_numerics {
   CGDR_NUMERICS_DEFAULT = 0,
   CGDR_NUMERICS_CONTEST = 1
 } cgdr_numerics;
+
+/* Optional overrides of the launch plan (cgdr_fwd_h_args.tuning; NULL = the library's plan).
+ * Every field has a "library's choice" value, so a zero-initialised struct with helpers,
+ * prefetch and helper_lead set to -1 changes nothing.  Results never depend on these fields
+ * (outputs are bit-identical for every V-tile, depth, load-wave count and helper setting);
+ * they exist for tests, benchmarks and devices the library has not been tuned on.  There is
+ * no counterpart in the reference: its tiling function picks one plan per shape. */
+typedef struct cgdr_fwd_h_tuning {
+  int32_t v_tile;        /* 0: library's choice; else 16, 32 or 64 value columns per task    */
+  int32_t helpers;       /* -1: library's choice; 0: off; 1: on when tasks + helpers fit     */
+  int32_t load_waves;    /* 0: library's choice; else 1, 2 or 4 (bf16 kernel)                 */
+  int32_t stages;        /* 0: library's choice; else 2, 3 or 4 LDS stages (bf16 kernel)      */
+  int32_t prefetch;      /* -1: library's choice; L2 touch distance in chunks without helpers */
+  int32_t helper_lead;   /* -1: library's choice; chunks a helper runs ahead of its task       */
+  int32_t helper_waves;  /* 0: library's choice; waves per helper workgroup                   */
+  int32_t cu_count;      /* 0: the current device's compute units; else plan for this count  */
+  int32_t xcd_count;     /* 0: the current device's XCDs (accelerator complex dies)          */
+  int32_t reserved;      /* must be 0                                                          */
+} cgdr_fwd_h_tuning;
 
 /* Arguments of one FwdH call.  Field meaning follows the Triton wrapper
  * (docs/problem.txt:436-472): k [B,T,Hg,K], w [B,T,H,K], u [B,T,H,V], g [B,T,H],
@@ -112,6 +131,8 @@ typedef struct cgdr_fwd_h_args {
   int64_t stride_v[3];          /* (b, t, head) of v_new                                   */
   int64_t stride_h0[2];         /* (n, head); each K x V block contiguous                  */
   int64_t stride_final[2];      /* (n, head); each K x V block contiguous                  */
+
+  const cgdr_fwd_h_tuning* tuning; /* nullable (host memory): plan overrides, see above    */
 } cgdr_fwd_h_args;
 
 /* Phase 1 (host only, no device access): validate the arguments and report the
@@ -142,6 +163,10 @@ typedef struct cgdr_fwd_h_plan {
   int32_t stages;       /* LDS pipeline depth in chunks                              */
   int32_t lds_bytes;    /* LDS per workgroup                                          */
   int64_t workgroups;   /* grid size                                                  */
+  int32_t helpers;      /* 1: one L2-prefetch helper workgroup beside every task        */
+  int32_t load_waves;   /* DMA waves per task workgroup (bf16 kernel)                   */
+  int32_t cu_count;     /* compute units the plan was made for                          */
+  int32_t xcd_count;    /* XCDs the plan was made for                                   */
 } cgdr_fwd_h_plan;
 
 cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* plan);

@@ -20,10 +20,11 @@ What it restates (paths relative to the reference's
   (``docs/problem.txt:330-432``, "O1"): ``bf16(S)`` feeds ``W @ S`` and the h
   snapshot (``:356-360``, ``:392-394``), ``v_new`` is stored in the input dtype
   (``:396-398``), the gated value is rounded to bf16 before ``K^T @ .``
-  (``:401-405``) and the state stays fp32.  Parity unpinned beyond bf16 tolerance: the
-  placement of these rounding points is restated from the kernel text, which cannot run
-  here; the tests pin ``bf16_round`` bit for bit against torch and the rounded loop only to
-  within bf16 tolerance of the exact one.
+  (``:401-405``) and the state stays fp32.  The kernel text cannot run here; every one of
+  these rounding points is pinned by closed forms on one-hot operands, where each
+  contraction has a single nonzero product and so is exact in any summation order
+  (``tests/o1_probe.py``, ``tests/test_oracle.py``): moving any one of them (the
+  ``mistake`` variants below) breaks the closed form.
 * ``fwd_h_o2`` -- the contest reference ``run()`` / the golden generator's
   ``run_reference`` ("O2", ``code/tests/golden/generate_golden.py:350-440``,
   ``docs/problem.txt:81-167``): bf16 state, bf16 GEMM outputs, saturating fp16 casts
@@ -179,6 +180,7 @@ def fwd_h(
     rounding: str | None = None,
     compute_dtype=np.float32,
     save_new_value: bool = True,
+    mistake: str | None = None,
 ):
     """Chunked gated delta-rule state recurrence, token-major layouts.
 
@@ -189,12 +191,22 @@ def fwd_h(
 
     Returns ``(h, v_new, final)`` as arrays of ``compute_dtype``; ``h`` and
     ``v_new`` are already rounded to bf16 values when ``rounding="bf16"``.
+
+    ``mistake`` moves one rounding point of the bf16 model, for the tests that show the
+    closed-form pins catch such a change (never used to produce a reference):
+    ``"mm1_fp32_state"`` feeds the unrounded state to ``W @ S``; ``"gate_rounded_v_new"``
+    gates the bf16-rounded v_new (``bf16(bf16(Vn) gamma)``); ``"mm2_fp32_operand"`` leaves
+    the gated value unrounded in ``K^T @ .``; ``"bf16_state"`` rounds the carried state to
+    bf16 after every chunk.
     """
     if chunk_size != CHUNK_SIZE:
         raise ValueError(f"chunk_size must be {CHUNK_SIZE}, got {chunk_size}")
     if rounding not in (None, "bf16"):
         raise ValueError(f"unknown rounding {rounding!r}")
     rnd = bf16_round if rounding == "bf16" else (lambda a: a)
+    mistakes = (None, "mm1_fp32_state", "gate_rounded_v_new", "mm2_fp32_operand", "bf16_state")
+    if mistake not in mistakes or (mistake is not None and rounding != "bf16"):
+        raise ValueError(f"mistake must be one of {mistakes} (with rounding='bf16'), got {mistake!r}")
     cd = np.dtype(compute_dtype)
 
     k = np.asarray(k, dtype=cd)
@@ -224,23 +236,28 @@ def fwd_h(
             t1 = min(t0 + chunk_size, eos)
             Sr = rnd(S) if rounding else S
             h_out[b, boh + c] = Sr
+            if mistake == "mm1_fp32_state":
+                Sr = S
             Kc = np.transpose(k[b, t0:t1][:, head_of_key, :], (1, 0, 2))   # [H, L, K]
             Wc = np.transpose(w[b, t0:t1], (1, 0, 2))                       # [H, L, K]
             Uc = np.transpose(u[b, t0:t1], (1, 0, 2))                       # [H, L, V]
             Vn = Uc - np.matmul(Wc, Sr)                                     # [H, L, V]
             if save_new_value:
                 v_out[b, t0:t1] = np.transpose(rnd(Vn) if rounding else Vn, (1, 0, 2))
+            Vg = rnd(Vn) if mistake == "gate_rounded_v_new" else Vn
             if gq is not None:
                 gc = np.transpose(gq[b, t0:t1], (1, 0))                     # [H, L]
                 g_last = gc[:, -1]
                 gamma = safe_exp(g_last[:, None] - gc).astype(cd)
-                Vd = Vn * gamma[:, :, None]
+                Vd = Vg * gamma[:, :, None]
                 S = S * np.exp(g_last).astype(cd)[:, None, None]
             else:
-                Vd = Vn
-            if rounding:
+                Vd = Vg
+            if rounding and mistake != "mm2_fp32_operand":
                 Vd = rnd(Vd)
             S = S + np.matmul(np.transpose(Kc, (0, 2, 1)), Vd)
+            if mistake == "bf16_state":
+                S = rnd(S)
         if output_final_state:
             final[n] = S
     return h_out, v_out, final

@@ -3,6 +3,8 @@ NaN-canaried output buffers, and the tolerance check."""
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import torch
 
@@ -27,8 +29,9 @@ _DT = {torch.bfloat16: _abi.CGDR_BF16, torch.float32: _abi.CGDR_F32}
 
 
 def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=torch.float32,
-             canary=float("nan")):
-    """Token-major FwdH through the C ABI into output buffers pre-filled with `canary`."""
+             canary=float("nan"), tuning: dict | None = None):
+    """Token-major FwdH through the C ABI into output buffers pre-filled with `canary`;
+    `tuning` (fields of cgdr_fwd_h_tuning) overrides the launch plan."""
     k, w, u, g, h0, cu = d["k"], d["w"], d["u"], d["g"], d["initial_state"], d["cu_seqlens"]
     B, T, Hg, K = k.shape
     H, V = u.shape[2], u.shape[3]
@@ -69,6 +72,9 @@ def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=
         a.stride_h0[:] = list(h0.stride()[:2])
     if f is not None:
         a.stride_final[:] = list(f.stride()[:2])
+    if tuning:
+        t = _abi.make_tuning(**tuning)
+        a.tuning = ctypes.pointer(t)
     nws = _abi.workspace_size(a)
     ws = torch.full((max(nws, 1),), 0xAB, dtype=torch.uint8, device=k.device)
     _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream, ws.data_ptr() if nws else 0, nws)

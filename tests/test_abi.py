@@ -52,8 +52,11 @@ int main(void) {
   F(cgdr_chunk_o_args, in_dtype); F(cgdr_chunk_o_args, stride_q); F(cgdr_chunk_o_args, stride_o);
   F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
   F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, numerics); F(cgdr_fwd_h_args, stride_k);
-  F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final);
-  F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups);
+  F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final); F(cgdr_fwd_h_args, tuning);
+  F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups); F(cgdr_fwd_h_plan, helpers);
+  F(cgdr_fwd_h_plan, xcd_count);
+  F(cgdr_fwd_h_tuning, helpers); F(cgdr_fwd_h_tuning, cu_count); F(cgdr_fwd_h_tuning, reserved);
+  printf("tuning %zu\n", sizeof(cgdr_fwd_h_tuning));
   return 0;
 }''')
     exe = tmp_path / "layout"
@@ -65,8 +68,9 @@ int main(void) {
     assert int(out["plan"]) == ctypes.sizeof(_abi.FwdHPlan)
     assert int(out["ochunk"]) == ctypes.sizeof(_abi.ChunkOArgs)
     assert int(out["wy"]) == ctypes.sizeof(_abi.WyArgs)
+    assert int(out["tuning"]) == ctypes.sizeof(_abi.FwdHTuning)
     classes = {"cgdr_fwd_h_args": _abi.FwdHArgs, "cgdr_fwd_h_plan": _abi.FwdHPlan, "cgdr_chunk_o_args": _abi.ChunkOArgs,
-               "cgdr_wy_args": _abi.WyArgs}
+               "cgdr_wy_args": _abi.WyArgs, "cgdr_fwd_h_tuning": _abi.FwdHTuning}
     for key, val in out.items():
         if "." in key:
             s, f = key.split(".")
@@ -74,8 +78,11 @@ int main(void) {
             assert getattr(cls, f).offset == int(val), key
 
 
-def _args(B=1, T=256, H=4, Hg=2, K=128, V=128, dtype=_abi.CGDR_BF16, varlen=None):
+def _args(B=1, T=256, H=4, Hg=2, K=128, V=128, dtype=_abi.CGDR_BF16, varlen=None, tuning=None):
     a = _abi.FwdHArgs()
+    if tuning is not None:
+        a._keep = _abi.make_tuning(**tuning)
+        a.tuning = ctypes.pointer(a._keep)
     fake = 1 << 24     # aligned, never dereferenced: validation is host-only
     a.k = a.w = a.u = a.h = fake
     a.B, a.T, a.H, a.Hg, a.K, a.V = B, T, H, Hg, K, V
@@ -123,7 +130,8 @@ def test_token_major_g_needs_head_major_workspace(lib):
     # varlen, 2 sequences x 3 heads: one chunk per sequence, too short for helper workgroups
     assert _status(_with_g(_args(varlen=[0, 61, 64], T=64, H=3, Hg=1)))[1] == 3 * 64 * 4
     # 2 sequences of 96 and 100 chunks x 3 heads x 4 V-tiles = 24 tasks: helpers, 24 progress lines
-    assert _status(_with_g(_args(varlen=[0, 6144, 12544], T=12544, H=3, Hg=1)))[1] == 3 * 12544 * 4 + 24 * 128
+    assert _status(_mi355x(_with_g(_args(varlen=[0, 6144, 12544], T=12544, H=3, Hg=1))))[1] == \
+        3 * 12544 * 4 + 24 * 128
 
 
 def test_contest_numerics_need_one_flag_per_head(lib):
@@ -211,34 +219,76 @@ def test_host_chunk_metadata_rejects_bad_cu(lib):
         _abi.prepare_chunk_offsets([0, 5, 3])
 
 
+def _mi355x(a, **kw):
+    """Plan as for MI355X (256 CUs, 8 XCDs), whatever device this host has."""
+    t = _abi.make_tuning(cu_count=256, xcd_count=8, **kw)
+    a.tuning = ctypes.pointer(t)
+    a._keep = t
+    return a
+
+
 def test_plan_headline_fills_the_chip(lib):
     # 32 heads x 4 V-tiles of 32 columns, each task with an L2-prefetch helper workgroup on
     # its XCD: 256 workgroups, one per CU
-    p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128))
+    p = _abi.get_plan(_mi355x(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128)))
+    assert p.cu_count == 256 and p.xcd_count == 8 and p.helpers == 1
     assert p.kernel == 0 and p.v_tile == 32 and p.workgroups == 256
     assert p.lds_bytes <= 160 * 1024
     # helpers need the doubled grid to fit the chip and tasks in multiples of 8 (per XCD);
     # without them, 32-column tiles when 16-column ones would take more than one round of
     # the chip at one task workgroup per CU
-    p = _abi.get_plan(_args(B=2, T=4096, H=32, Hg=32, K=128, V=128))
+    p = _abi.get_plan(_mi355x(_args(B=2, T=4096, H=32, Hg=32, K=128, V=128)))
     assert p.v_tile == 32 and p.workgroups == 2 * 32 * 4
-    p = _abi.get_plan(_args(B=1, T=8192, H=16, Hg=16, K=128, V=128))   # 128 tasks of 16 columns
-    assert p.v_tile == 32 and p.workgroups == 2 * 16 * 4                # helper mode
-    p = _abi.get_plan(_args(B=1, T=8192, H=6, Hg=6, K=128, V=128))
+    p = _abi.get_plan(_mi355x(_args(B=1, T=8192, H=16, Hg=16, K=128, V=128)))   # 128 tasks of 16 columns
+    assert p.v_tile == 32 and p.workgroups == 2 * 16 * 4                         # helper mode
+    p = _abi.get_plan(_mi355x(_args(B=1, T=8192, H=6, Hg=6, K=128, V=128)))
     assert p.workgroups == 6 * 8
     # sequences under 96 chunks: no helpers, 16-column tiles while they fit one round
-    p = _abi.get_plan(_args(B=1, T=4096, H=16, Hg=16, K=128, V=128))
+    p = _abi.get_plan(_mi355x(_args(B=1, T=4096, H=16, Hg=16, K=128, V=128)))
     assert p.v_tile == 16 and p.workgroups == 16 * 8
+
+
+def test_plan_follows_the_device_topology(lib):
+    """The plan is made for the device's CU and XCD counts: on a smaller device (a partition
+    of 64 CUs in 2 XCDs) the headline's 128 tasks + 128 helpers no longer fit, so it runs
+    without helpers; helpers come back when the tasks fit half the CUs and split evenly over
+    the XCDs, and stay off when they do not split evenly."""
+    a = _args(B=1, T=32768, H=32, Hg=32, K=128, V=128)
+    a.tuning = ctypes.pointer(t := _abi.make_tuning(cu_count=64, xcd_count=2))
+    p = _abi.get_plan(a)
+    assert (p.cu_count, p.xcd_count, p.helpers) == (64, 2, 0)
+    assert (p.v_tile, p.workgroups) == (32, 128)
+    p = _abi.get_plan(_args(B=1, T=32768, H=8, Hg=8, K=128, V=128, tuning=dict(cu_count=64, xcd_count=2)))
+    assert (p.helpers, p.v_tile, p.workgroups) == (1, 32, 2 * 8 * 4)
+    p = _abi.get_plan(_args(B=1, T=32768, H=5, Hg=5, K=128, V=128, tuning=dict(cu_count=64, xcd_count=8)))
+    assert p.helpers == 0          # 20 tasks of 32 columns do not split over 8 XCDs
+    p = _abi.get_plan(_args(B=1, T=32768, H=8, Hg=8, K=128, V=128, tuning=dict(cu_count=64, xcd_count=8)))
+    assert p.helpers == 1 and p.workgroups == 64
+    del t
+
+
+def test_tuning_overrides_and_rejections(lib):
+    """Explicit plan overrides take effect, and out-of-range values are rejected."""
+    p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128,
+                            tuning=dict(cu_count=256, xcd_count=8, helpers=0, v_tile=16)))
+    assert (p.helpers, p.v_tile, p.workgroups) == (0, 16, 256)
+    p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128,
+                            tuning=dict(cu_count=256, xcd_count=8, load_waves=1, stages=2)))
+    assert (p.load_waves, p.stages) == (1, 2)
+    for bad in (dict(v_tile=48), dict(helpers=2), dict(load_waves=3), dict(stages=5), dict(reserved=1),
+                dict(cu_count=-1)):
+        a = _args(tuning=bad)
+        assert _status(a)[0] == _abi.CGDR_ERR_INVALID, bad
 
 
 def test_helper_mode_workspace_holds_progress_counters(lib):
     # one 128-byte progress line per task, after the (256-byte rounded) head-major g copy
     # (helpers from 96 chunks per sequence on)
-    a = _args(B=1, T=6100, H=32, Hg=32, K=128, V=128)
+    a = _mi355x(_args(B=1, T=6100, H=32, Hg=32, K=128, V=128))
     assert _status(a) == (_abi.CGDR_OK, 128 * 128)
-    a = _with_g(_args(B=1, T=6100, H=32, Hg=32, K=128, V=128))
+    a = _mi355x(_with_g(_args(B=1, T=6100, H=32, Hg=32, K=128, V=128)))
     assert _status(a) == (_abi.CGDR_OK, ((32 * 6100 * 4 + 255) // 256) * 256 + 128 * 128)
-    assert _status(_args(B=1, T=6000, H=32, Hg=32, K=128, V=128)) == (_abi.CGDR_OK, 0)   # 94 chunks
+    assert _status(_mi355x(_args(B=1, T=6000, H=32, Hg=32, K=128, V=128))) == (_abi.CGDR_OK, 0)   # 94 chunks
 
 
 def test_wrapper_refuses_cpu_tensors():

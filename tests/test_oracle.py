@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+import o1_probe
 from oracle import cgdr_oracle as O
 
 
@@ -212,3 +213,42 @@ def test_varlen_lengths_avoid_chunk_multiples():
     cu = O.varlen_cu_seqlens(0, 16, 64, 8192)
     lens = np.diff(cu)
     assert len(lens) == 16 and np.all(lens % 64 != 0) and lens.min() >= 64 and lens.max() <= 8192
+
+
+# ---------------------------------------------------------------- O1 rounding points
+
+O1_MISTAKES = ("mm1_fp32_state", "gate_rounded_v_new", "mm2_fp32_operand", "bf16_state")
+
+
+@pytest.mark.parametrize("K,V,n_chunks,H", [(32, 32, 3, 2), (128, 128, 4, 2), (64, 48, 3, 1)])
+def test_o1_rounding_points_closed_form(K, V, n_chunks, H):
+    """The bf16 model equals, bit for bit, the closed form of the Triton kernel's four rounding
+    rules on one-hot W and K rows (tests/o1_probe.py; docs/problem.txt:356-405): bf16(S) into
+    W @ S, v_new from the fp32 Vn before gating, bf16(Vn gamma) into K^T @ ., fp32 state."""
+    inp = o1_probe.probe_inputs(K, V, n_chunks, H=H, seed=1)
+    assert o1_probe.gamma_margin_ok(inp)
+    for name, want, got in zip(("h", "v_new", "final"), o1_probe.closed_form(inp), O.fwd_h(**inp, rounding="bf16")):
+        assert np.array_equal(want, got), name
+
+
+@pytest.mark.parametrize("mistake", O1_MISTAKES)
+def test_o1_closed_form_catches_moved_rounding_points(mistake):
+    """Each plausible misplacement of one rounding point breaks the closed form."""
+    inp = o1_probe.probe_inputs(32, 32, 3, H=2, seed=1)
+    want = o1_probe.closed_form(inp)
+    got = O.fwd_h(**inp, rounding="bf16", mistake=mistake)
+    assert any(not np.array_equal(a, b) for a, b in zip(want, got)), mistake
+
+
+def test_o1_probe_distinguishes_each_rule():
+    """The probe's values really exercise the rules: bf16 cannot hold the fp32 state rows,
+    the MM1 operand rounding changes v_new, and gamma differs from 1 on the gated tokens."""
+    inp = o1_probe.probe_inputs(32, 32, 2, H=1, seed=1)
+    h0 = inp["initial_state"]
+    assert (O.bf16_round(h0[0, 0, :16]) != h0[0, 0, :16]).all()
+    g = inp["g"][0, :16, 0]
+    assert (g > 0).all() and (inp["g"][0, 16:64, 0] == 0).all()
+    h, v_new, final = o1_probe.closed_form(inp)
+    assert np.array_equal(final[0, 0, :16], h0[0, 0, :16])          # fp32 state carried
+    u0 = inp["u"][0, 16:32, 0]
+    assert not np.array_equal(v_new[0, 16:32, 0], O.bf16_round(u0 - h0[0, 0, :16]))

@@ -99,8 +99,8 @@ static int rank_no_tiebreak(const int64_t* cu, int N, int n) {
 }
 
 // The kernel's order_task on the host: the lane whose sequence has rank r (N <= 64), else r.
-static int order(const std::vector<int64_t>& cu, int N, int H, int nv, int d, bool naive) {
-  const VarlenSlot s = varlen_slot(d, N * H * nv, H, nv);
+static int order(const std::vector<int64_t>& cu, int N, int H, int nv, int nx, int d, bool naive) {
+  const VarlenSlot s = varlen_slot(d, N * H * nv, H, nv, nx);
   int n = s.rank;
   if (N <= 64) {
     n = -1;
@@ -116,6 +116,7 @@ static int order(const std::vector<int64_t>& cu, int N, int H, int nv, int d, bo
 int main() {
   std::mt19937 rng(7);
   int cases = 0, bad = 0, naive_bad = 0;
+  for (int nx : {8, 4, 2, 1})
   for (int N : {1, 2, 3, 5, 16, 17, 63, 64, 65, 100})
     for (int H : {8, 16, 32, 64})
       for (int nv : {1, 2, 4, 8})
@@ -126,28 +127,28 @@ int main() {
             const int64_t L = trial == 0 ? 64 * (int64_t)(rng() % 3) : (int64_t)(rng() % 9000);
             cu[i + 1] = cu[i] + L;
           }
-          const int T = N * H * nv, q = T / 8, hx = H / 8;
+          const int T = N * H * nv, q = T / nx, hx = H / nx;
           std::vector<int> seen(T, 0), seen_naive(T, 0);
           bool ok = true, ok_naive = true;
           for (int d = 0; d < T; ++d) {
-            const int t = order(cu, N, H, nv, d, false), tn = order(cu, N, H, nv, d, true);
+            const int t = order(cu, N, H, nv, nx, d, false), tn = order(cu, N, H, nv, nx, d, true);
             if (t < 0 || t >= T || seen[t]++) ok = false;
             if (tn < 0 || tn >= T || seen_naive[tn]++) ok_naive = false;
             if (!ok) break;
             const int x = d / q, head = (t / nv) % H, n = t / nv / H;
             if (head / hx != x) ok = false;   // the block's own heads
             if (d % q > 0 && N <= 64) {       // within a block: lengths never increase
-              const int tp = order(cu, N, H, nv, d - 1, false), np = tp / nv / H;
+              const int tp = order(cu, N, H, nv, nx, d - 1, false), np = tp / nv / H;
               if (cu[np + 1] - cu[np] < cu[n + 1] - cu[n]) ok = false;
             }
           }
           // every block gets the same work: hx heads x nv tiles of every sequence
-          std::vector<int64_t> work(8, 0);
+          std::vector<int64_t> work(nx, 0);
           for (int d = 0; ok && d < T; ++d) {
-            const int n = order(cu, N, H, nv, d, false) / nv / H;
+            const int n = order(cu, N, H, nv, nx, d, false) / nv / H;
             work[d / q] += cu[n + 1] - cu[n];
           }
-          for (int x = 1; ok && x < 8; ++x) if (work[x] != work[0]) ok = false;
+          for (int x = 1; ok && x < nx; ++x) if (work[x] != work[0]) ok = false;
           ++cases;
           bad += !ok;
           naive_bad += !ok_naive;
@@ -161,8 +162,9 @@ int main() {
 def test_varlen_dispatch_order_is_balanced_permutation(tmp_path):
     """The packed-batch dispatch order (cgdr_schedule.h varlen_slot / seq_rank, with the
     kernel's lane search) is a permutation of the tasks for N up to 100 sequences (ties and
-    empty sequences included); XCD block x holds heads [x H/8, (x+1) H/8) of every sequence,
-    so every block gets the same work; and within a block lengths never increase (N <= 64).
+    empty sequences included) and 8, 4, 2 or 1 XCDs; XCD block x holds heads
+    [x H/nx, (x+1) H/nx) of every sequence, so every block gets the same work; and within a
+    block lengths never increase (N <= 64).
     The rank without its tie-break must fail the permutation check on tied lengths."""
     src = tmp_path / "order.cpp"
     src.write_text(ORDER_DRIVER)
@@ -170,6 +172,6 @@ def test_varlen_dispatch_order_is_balanced_permutation(tmp_path):
     subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Werror", "-I", CSRC, str(src), "-o", str(exe)], check=True)
     cases, bad, naive_bad = map(int, subprocess.run([str(exe)], capture_output=True, text=True,
                                                     check=True).stdout.split())
-    assert cases == 10 * 4 * 4 * 3
+    assert cases == 4 * 10 * 4 * 4 * 3
     assert bad == 0
     assert naive_bad > 0, "the check must catch ranks without the tie-break"
