@@ -143,9 +143,15 @@ cgdr_status check_tuning(const cgdr_fwd_h_tuning* tu) {
   return CGDR_OK;
 }
 
-// Kernel variant and grid.  The bf16 pipeline needs K in {32,64,128,256} (MFMA contraction
-// slices of 32 and the LDS swizzles), V a multiple of 16, 16-byte aligned rows of k/w/u
-// (direct-to-LDS loads move 16 bytes per lane) and 8-byte aligned rows of h/v_new.
+// The key dim the kernels are instantiated for: K rounded up to 32, 64, 128 or 256 (MFMA
+// contraction slices of 32 and the LDS swizzles); the tiles' columns and the state's rows
+// past K are zero padding.
+int kernel_kd(int64_t K) { return K <= 32 ? 32 : K <= 64 ? 64 : K <= 128 ? 128 : 256; }
+
+// Kernel variant and grid.  The kernels need K a multiple of 16 (whole 16-row state tiles; the
+// reference accepts any K = V in [32, 256], _infershape.cpp:35-36,214-223), V a multiple of
+// 16, 16-byte aligned rows of k/w/u (direct-to-LDS loads move 16 bytes per lane) and 8-byte
+// aligned rows of h/v_new.
 cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   cgdr_status st = validate(a);
   if (st != CGDR_OK) return st;
@@ -154,12 +160,11 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   if (st != CGDR_OK) return st;
   const int64_t K = a->K, V = a->V;
   const int es = a->in_dtype == CGDR_BF16 ? 2 : 4;
-  if (!(K == 32 || K == 64 || K == 128 || K == 256))
-    return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (supported: 32, 64, 128, 256)", (long long)K);
+  if (K < 32 || K % 16 != 0)
+    return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (must be a multiple of 16 in [32, 256])", (long long)K);
+  const int kd = kernel_kd(K);
   if (V % 16 != 0)
     return fail(CGDR_ERR_UNSUPPORTED, "V=%lld is not supported (must be a multiple of 16)", (long long)V);
-  if (a->in_dtype == CGDR_F32 && K > 128)
-    return fail(CGDR_ERR_UNSUPPORTED, "fp32 inputs support K <= 128, got K=%lld", (long long)K);
   const int row_align = a->in_dtype == CGDR_BF16 ? 16 : 4;
   const void* ptrs[] = {a->k, a->w, a->u};
   const int64_t* strides[] = {a->stride_k, a->stride_w, a->stride_u};
@@ -190,7 +195,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   // task, when tasks and helpers together fit the device at one workgroup per CU (all
   // resident at once) and the tasks split evenly over the XCDs.
   const int helpers_req = tu != nullptr ? tu->helpers : -1;
-  const bool helper_shape = a->in_dtype == CGDR_BF16 && K <= 128 && V % 32 == 0 &&
+  const bool helper_shape = a->in_dtype == CGDR_BF16 && kd <= 128 && V % 32 == 0 &&
                             (pairs * (V / 32)) % xcds == 0 && 2 * pairs * (V / 32) <= cus;
   // Helpers pay only on long sequences: at B=1, H=32, K=V=128 they measured 64.7 vs 54.7 us
   // (16-column tiles, no helpers) at 64 chunks per sequence and 112 vs 143 us at 128.  A packed
@@ -222,7 +227,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   } else {
     // bf16: the pipelined kernel, with the contest rounding model when asked for
     pl->kernel = a->numerics == CGDR_NUMERICS_CONTEST ? 2 : 0;
-    if (K == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
+    if (kd == 256) ncw = 1;   // K=256 state and tiles leave LDS room for one compute wave only
     pl->ncw = ncw;
     int nlw = tu != nullptr ? tu->load_waves : 0;
     // With helper workgroups the task's loads are L2 hits and one load wave keeps up; at most
@@ -231,9 +236,9 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     // 32-column tiles without helpers: one load wave (with the L2 touches 2 chunks ahead,
     // below) measured 925 us against 1,020 us with two, for 16 packed sequences of lengths
     // U[64, 8192] at H=32, K=V=128.
-    if (nlw == 0) nlw = (use_helpers || K == 256 || ncw == 2) ? 1 : 2;
+    if (nlw == 0) nlw = (use_helpers || kd == 256 || ncw == 2) ? 1 : 2;
     if (pl->kernel == 2 && nlw == 4) nlw = 2;   // contest instantiations: 1 or 2 load waves
-    if (K == 256) nlw = 1;
+    if (kd == 256) nlw = 1;
     while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
     pl->nlw = nlw;
     int stages = tu != nullptr ? tu->stages : 0;
@@ -287,6 +292,7 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
     p.helper_waves = hw > max_hw ? max_hw : hw;
   }
   p.n_xcd = pl.xcds;
+  p.K = (int32_t)a->K;
   p.progress = nullptr;
   return p;
 }
@@ -324,7 +330,7 @@ int bf16_max_stages(int64_t K, int ncw, int nlw) {
     if (ncw == 2) return by_ncw(std::integral_constant<int, 2>{});
     return by_ncw(std::integral_constant<int, 1>{});
   };
-  switch (K) {
+  switch (kernel_kd(K)) {
     case 32: return pick(std::integral_constant<int, 32>{});
     case 64: return pick(std::integral_constant<int, 64>{});
     case 128: return pick(std::integral_constant<int, 128>{});
@@ -339,7 +345,7 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
       return pl.ncw == 1 ? cgdr::F32Layout<KD, 1>::LDS_BYTES
                          : pl.ncw == 2 ? cgdr::F32Layout<KD, 2>::LDS_BYTES : cgdr::F32Layout<KD, 4>::LDS_BYTES;
     };
-    switch (K) {
+    switch (kernel_kd(K)) {
       case 32: return f32(std::integral_constant<int, 32>{});
       case 64: return f32(std::integral_constant<int, 64>{});
       case 128: return f32(std::integral_constant<int, 128>{});
@@ -348,7 +354,7 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
   }
   // bf16: the layout of the instantiated kernel
   auto lds = [](auto layout) -> int { return decltype(layout)::LDS_BYTES; };
-  switch (K) {
+  switch (kernel_kd(K)) {
     case 32: return with_bf16_config<32>(pl, lds);
     case 64: return with_bf16_config<64>(pl, lds);
     case 128: return with_bf16_config<128>(pl, lds);
@@ -458,7 +464,7 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     e = hipGetLastError();
     if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "counter reset launch failed: %s", hipGetErrorString(e));
   }
-  switch (args->K) {
+  switch (kernel_kd(args->K)) {
     case 32: e = cgdr_fwd::launch_kd<32>(p, pl, s); break;
     case 64: e = cgdr_fwd::launch_kd<64>(p, pl, s); break;
     case 128: e = cgdr_fwd::launch_kd<128>(p, pl, s); break;

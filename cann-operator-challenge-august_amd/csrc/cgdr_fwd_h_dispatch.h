@@ -89,12 +89,9 @@ template <int KD>
 hipError_t launch_kd(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if (pl.kernel == 0) return dispatch_bf16<KD, 0>(p, pl, s);
   if (pl.kernel == 2) return dispatch_contest<KD>(p, pl, s);
-  if constexpr (KD <= 128) {
-    if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
-    if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
-    return launch_f32<KD, 1>(p, pl.tasks, s);
-  }
-  return hipErrorInvalidValue;   // the plan never selects the fp32 kernel above K = 128
+  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
+  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
+  return launch_f32<KD, 1>(p, pl.tasks, s);
 }
 
 extern template hipError_t launch_kd<32>(const cgdr::FwdHParams&, const Plan&, hipStream_t);

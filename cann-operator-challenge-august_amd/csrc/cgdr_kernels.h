@@ -104,6 +104,8 @@ struct FwdHParams {
   int32_t helper_lead;  // chunks a helper runs ahead of its task's load waves
   int32_t helper_waves; // waves per helper workgroup issuing touches
   int32_t n_xcd;        // XCDs workgroups are dealt to round-robin (blockIdx % n_xcd)
+  int32_t K;            // key dim, a multiple of 16 up to the kernel's KD: columns K..KD-1 of
+                        // the K and W tiles and rows K..KD-1 of the state are zero padding
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
                         // task (kProgressStride ints; zeroed before launch)
   int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
@@ -437,8 +439,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   const uint32_t trash = (uint32_t)(uintptr_t)((lds_char*)smem) + L::TRASH_OFF;
   auto l2_touch_setup = [&]() {
     const int nvt = p.n_vtiles;
-    const int seg = ((2 * KD) % 128 == 0 && (2 * p.V) % 128 == 0) ? 128 : ((2 * p.V) % 64 == 0 ? 64 : 32);
-    const int segk = 2 * KD / seg, segv = (int)(2 * p.V / seg);
+    const int kb = 2 * p.K, vb = (int)(2 * p.V);   // row bytes, multiples of 32
+    const int seg = (kb % 128 == 0 && vb % 128 == 0) ? 128 : ((kb % 64 == 0 && vb % 64 == 0) ? 64 : 32);
+    const int segk = kb / seg, segv = vb / seg;
     const int segs = 64 * (2 * segk + segv);
     const char* kpf = (const char*)((const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h);
     const char* wpf = (const char*)((const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h);
@@ -500,8 +503,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     };
     auto helper_touch = [&](int j) {
       const int64_t t0 = tk.bos + (int64_t)j * kChunk;
-      touch_rows(hk_base + t0 * hk_st, hk_st, 2 * KD);
-      touch_rows(hw_base + t0 * hw_st, hw_st, 2 * KD);
+      touch_rows(hk_base + t0 * hk_st, hk_st, 2 * p.K);
+      touch_rows(hw_base + t0 * hw_st, hw_st, 2 * p.K);
       touch_rows(hu_base + t0 * hu_st, hu_st, (int)(2 * p.V));
       if (hg_base != nullptr && tk.vtile == 0) dma_b32(hg_base + t0 * hg_st, (uint32_t)(lane * hg_st), hscratch);
     };
@@ -545,8 +548,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
           const int64_t off = base + (int64_t)krow * p.V + vcol;
-          S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off]
-                              : bf16_lo(((const unsigned short*)p.h0)[off]);
+          S[kt][r] = krow >= p.K ? 0.f
+                     : p.h0_f32 ? ((const float*)p.h0)[off]
+                                : bf16_lo(((const unsigned short*)p.h0)[off]);
           if constexpr (CONTEST) S[kt][r] = bf16_rnd(S[kt][r]);   // the state is bf16
         }
     } else {
@@ -773,6 +777,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
           const int64_t off = base + (int64_t)krow * p.V + vcol;
+          if (krow >= p.K) continue;
           if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
           else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
         }
@@ -795,12 +800,18 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     constexpr int PU = VT / 8;                  // U pieces per row
     const int lrow = lane / P, lcol = lane % P;
     const int64_t stw = p.sw_t * 2, stk = p.sk_t * 2, stu = p.su_t * 2;   // row strides in bytes
+    // A key dim K below KD: the pieces at or past K/8 of a row are padding.  Their lanes load
+    // piece 0 of the row instead (in bounds, same cache line as a real piece), and once the
+    // chunk has landed the load wave overwrites those LDS slots with zeros (zero_padding).
+    const int kp = p.K / 8;
+    const bool padded = kp < P;
     uint32_t woff[L::DMA_W], koff[L::DMA_W], uoff[L::DMA_U];
 #pragma unroll
     for (int m = 0; m < L::DMA_W; ++m) {
       const int r = m * RPI + lrow;
-      woff[m] = (uint32_t)(r * stw) + 16u * (uint32_t)(lcol ^ swz_w<P>(r));
-      koff[m] = (uint32_t)(r * stk) + 16u * (uint32_t)(lcol ^ swz_k<P>(r));
+      const int gw = lcol ^ swz_w<P>(r), gk = lcol ^ swz_k<P>(r);
+      woff[m] = (uint32_t)(r * stw) + 16u * (uint32_t)(gw < kp ? gw : 0);
+      koff[m] = (uint32_t)(r * stk) + 16u * (uint32_t)(gk < kp ? gk : 0);
     }
 #pragma unroll
     for (int m = 0; m < L::DMA_U; ++m) {
@@ -862,6 +873,21 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       };
 
+      // Zero this wave's padding slots of the W and K tiles in stage st, once its DMAs of the
+      // chunk there have landed (each wave zeroes the slots of its own DMA instructions).
+      auto zero_padding = [&](int st) {
+        if (!padded) return;
+        char* sbase = smem + st * L::STAGE_BYTES;
+#pragma unroll
+        for (int m = 0; m < L::DMA_W; ++m) {
+          const int r = m * RPI + lrow;
+          if ((m % NLW) == LW && (lcol ^ swz_w<P>(r)) >= kp)
+            *(u32x4*)(sbase + L::W_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+          if (((L::DMA_W + m) % NLW) == LW && (lcol ^ swz_k<P>(r)) >= kp)
+            *(u32x4*)(sbase + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+        }
+      };
+
       // Schedule.  D = STAGES - 1 chunks are in flight ahead of the compute waves.  Each loop
       // iteration first issues chunk c+D (into the stage the last barrier freed), then waits
       // for chunk c+1.  vmcnt completes loads in order, so that wait is "at most D-1 full
@@ -878,6 +904,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         for (int j = 0; j < D && j < NC; ++j) issue(j, j);
         if (sched::prologue_allowance(D, NC) > 0) wait_vm<STEADY_VM>();
         else wait_vm<0>();
+        zero_padding(0);
       }
       wait_lgkm0();
       block_barrier();   // P
@@ -887,8 +914,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         if (c + 1 < NC) {
           if (sched::loop_allowance(c, D, NC) > 0) wait_vm<STEADY_VM>();
           else wait_vm<0>();
+          zero_padding((c + 1) % STAGES);
         }
-        wait_lgkm0();      // zero-fill writes of a partial chunk
+        wait_lgkm0();      // zero-fill writes of a partial chunk and of padding
         block_barrier();   // B_c
       }
     };
@@ -942,7 +970,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           hv[2 * half + 1] = x[1] ^ 0x80008000u;
           if constexpr (NUM == 1) amax = pk_absmax_bf16(pk_absmax_bf16(amax, x[0]), x[1]);
         }
-        *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;
+        if (k0 < p.K) *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;   // rows >= K: padding
       }
       if (vbase_ptr != nullptr || NUM == 1) {
         const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
@@ -1115,7 +1143,8 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       for (int r = 0; r < 4; ++r) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (int64_t)krow * p.V + vcol;
-        S[kt][r] = p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
+        S[kt][r] = krow >= p.K ? 0.f
+                   : p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
       }
   } else {
 #pragma unroll
@@ -1129,8 +1158,9 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     {
       for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
         const int r = idx / KD, col = idx % KD;
-        Ws[r * WP + col] = r < len ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
-        Ks[r * WP + col] = r < len ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
+        const bool ok = r < len && col < p.K;   // zero rows past the end and padding columns
+        Ws[r * WP + col] = ok ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
+        Ks[r * WP + col] = ok ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
       }
       for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
         const int r = idx / VT, col = idx % VT;
@@ -1159,7 +1189,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-          hdst[(int64_t)krow * p.V + vcol] = (E)S[kt][r];
+          if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[kt][r];
         }
     }
     // MM1: acc[tt] = W S   (contraction slot g of step (kt, r) is k = pi(kt, 4g + r))
@@ -1211,6 +1241,7 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       for (int r = 0; r < 4; ++r) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (int64_t)krow * p.V + vcol;
+        if (krow >= p.K) continue;
         if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
         else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
       }

@@ -170,7 +170,8 @@ def test_launch_rejects_missing_or_short_workspace(lib):
     (lambda a: setattr(a, "NT", 5), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "N", 2), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "K", 300), _abi.CGDR_ERR_INVALID),         # K > 256
-    (lambda a: setattr(a, "K", 96), _abi.CGDR_ERR_UNSUPPORTED),
+    (lambda a: setattr(a, "K", 100), _abi.CGDR_ERR_UNSUPPORTED),   # not a multiple of 16
+    (lambda a: setattr(a, "K", 16), _abi.CGDR_ERR_UNSUPPORTED),    # below 32
     (lambda a: setattr(a, "V", 24), _abi.CGDR_ERR_UNSUPPORTED),
     (lambda a: setattr(a, "in_dtype", 7), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "k", (1 << 24) + 8), _abi.CGDR_ERR_UNSUPPORTED),   # DMA needs 16B rows
@@ -265,6 +266,31 @@ def test_plan_follows_the_device_topology(lib):
     p = _abi.get_plan(_args(B=1, T=32768, H=8, Hg=8, K=128, V=128, tuning=dict(cu_count=64, xcd_count=8)))
     assert p.helpers == 1 and p.workgroups == 64
     del t
+
+
+@pytest.mark.parametrize("K,V,kd_plan", [(48, 48, dict(v_tile=16)), (96, 96, dict(v_tile=32, helpers=1)),
+                                          (160, 160, dict(v_tile=16, helpers=0)), (224, 224, dict(v_tile=16)),
+                                          (96, 128, dict(v_tile=32))])
+def test_plan_accepts_padded_head_dims(lib, K, V, kd_plan):
+    """Key dims that are multiples of 16 between the kernels' 32, 64, 128 and 256 are accepted
+    (the reference takes any K = V in [32, 256]) and planned as the next instantiated key dim:
+    K = 160 and 224 run the K = 256 layout (one compute wave, 16 columns, no helpers)."""
+    a = _mi355x(_args(B=1, T=32768, H=32, Hg=32, K=K, V=V))
+    st, _ = _status(a)
+    assert st == _abi.CGDR_OK, _abi.last_error()
+    p = _abi.get_plan(a)
+    for key, want in kd_plan.items():
+        assert getattr(p, key) == want, (K, V, key, getattr(p, key))
+    a.in_dtype = _abi.CGDR_F32
+    assert _status(a)[0] == _abi.CGDR_OK, _abi.last_error()   # fp32 up to K = 256
+
+
+@pytest.mark.parametrize("B,T,H,K", [(5, 2000, 32, 32), (4, 4000, 32, 64)])
+def test_plan_wide_tiles_without_helpers(lib, B, T, H, K):
+    """The shapes of test_gpu_parity.test_default_plan_wide_tiles_without_helpers plan 32-column
+    tiles with one load wave and no helpers on MI355X."""
+    p = _abi.get_plan(_mi355x(_args(B=B, T=T, H=H, Hg=H, K=K, V=K)))
+    assert (p.v_tile, p.helpers, p.load_waves) == (32, 0, 1)
 
 
 def test_tuning_overrides_and_rejections(lib):

@@ -281,6 +281,33 @@ def test_contest_kernel_saturation(dev):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("D", [48, 96, 160, 192])
+def test_contest_kernel_padded_head_dims(dev, D):
+    """Contest numerics at key dims between the kernels' instantiated 32/64/128/256 (zero-padded
+    tiles and state rows on chip): against the O2 oracle, with the generator's distributions
+    (generate_golden.py: k, u in [-1, 1), w in [-1, 1)/D, a linear chunk-local gate), grouped
+    heads and two sequences, one ending in a partial chunk."""
+    print(f"[contest] D={D}", flush=True)
+    rng = np.random.default_rng(100 + D)
+    T, HV, HK = 200, 4, 2
+    k = O.bf16_round((rng.random((1, T, HK, D)) * 2 - 1).astype(np.float32))
+    w = O.bf16_round(((rng.random((1, HV, T, D)) * 2 - 1) / D).astype(np.float32))
+    u = O.bf16_round((rng.random((1, HV, T, D)) * 2 - 1).astype(np.float32))
+    h0 = O.bf16_round((rng.random((2, HV, D, D)) * 2 - 1).astype(np.float32))
+    cu = np.array([0, 128, 200], np.int64)
+    g = np.zeros((1, HV, T), np.float32)
+    for i0, i1 in ((0, 64), (64, 128), (128, 192), (192, 200)):
+        g[..., i0:i1] = -0.02 * np.arange(1, i1 - i0 + 1, dtype=np.float32)
+    a = dict(input_k=k, input_w=w, input_u=u, input_g=g, input_initial_state=h0, input_cu_seqlens=cu)
+    got = _run_contest(dev, a)
+    ref = O.fwd_h_o2(k, w, u, g, h0, cu)
+    for name, x, r in zip(("h", "v", "final"), got, ref):
+        exact = (x == r).mean()
+        assert exact >= O2_MIN_EXACT, (D, name, exact)
+        assert np.abs(x - r).max() <= 1e-2 * np.abs(r).max(), (D, name)
+
+
+@pytest.mark.gpu
 def test_contest_kernel_without_v_new_output(dev):
     """Token-major calls, u beyond the fp16 range on one head: that shows first in the staged
     v_new, which the fast pass checks whether or not v_new is an output.  With v_new requested

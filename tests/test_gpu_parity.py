@@ -119,13 +119,18 @@ def test_config4_full_size(dev):
 
 # ---------------------------------------------------------------- shapes and edge cases
 
-@pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (64, 128), (128, 64), (256, 256), (256, 64)])
+# K = 48 ... 224: key dims between the kernels' 32, 64, 128 and 256, whose K and W tiles and state
+# rows are zero-padded on chip (the reference accepts any K = V in [32, 256])
+@pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (64, 128), (128, 64), (256, 256), (256, 64),
+                                 (48, 48), (80, 80), (96, 96), (112, 112), (160, 160), (192, 192), (224, 224),
+                                 (96, 128)])
 def test_head_dims_bf16(dev, K, V):
     inp = _case(10 + K + V, 1, 200, 2, K, V, shift=4.0, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
-@pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (128, 128), (128, 64)])
+@pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (128, 128), (128, 64), (48, 48), (96, 96), (192, 192),
+                                 (256, 256)])
 def test_head_dims_fp32(dev, K, V):
     inp = _case(20 + K + V, 2, 130, 2, K, V, dtype="f32", gate="linear")
     out = abi_call(dev_inputs(inp, torch.float32, dev))
@@ -133,17 +138,73 @@ def test_head_dims_fp32(dev, K, V):
         assert_close(np32(got), ref, name=name, **F32_TOL)
 
 
+# The pipeline variants a partial chunk meets: 16- and 32-column V-tiles (two load waves and
+# one by default), each with and without L2-prefetch helper workgroups (the task counts below
+# split over the 8 XCDs and fit the chip twice over, so a requested helper runs).
+PLANS = [dict(v_tile=16, helpers=0), dict(v_tile=16, helpers=1), dict(v_tile=32, helpers=0),
+         dict(v_tile=32, helpers=1)]
+PLAN_IDS = ["vt16", "vt16-helpers", "vt32", "vt32-helpers"]
+
+
+@pytest.mark.parametrize("plan", PLANS, ids=PLAN_IDS)
 @pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 127, 128, 129])
-def test_chunk_boundaries(dev, T):
+def test_chunk_boundaries(dev, T, plan):
     inp = _case(30 + T, 2, T, 2, 64, 64, shift=4.0, profile="wy")
+    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev), tuning=plan), inp)
+
+
+@pytest.mark.parametrize("plan", PLANS, ids=PLAN_IDS)
+@pytest.mark.parametrize("lens", [[1], [61, 3], [63, 64, 65], [1, 70, 128, 129], [5, 64, 129, 1023],
+                                  [127, 128, 129, 1, 2, 3, 300]])
+def test_varlen_cases(dev, lens, plan):
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(40 + len(lens), 1, int(cu[-1]), 4, 64, 64, Hg=2, shift=4.0, cu=cu, profile="wy")
+    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev), tuning=plan), inp)
+
+
+@pytest.mark.parametrize("B,T,H,K", [(5, 2000, 32, 32), (4, 4000, 32, 64)])
+def test_default_plan_wide_tiles_without_helpers(dev, B, T, H, K):
+    """K = V = 32 and 64 at shapes whose default plan is 32-column tiles, one load wave, no
+    helpers (more tasks than half the chip; sequences of 32 and 63 chunks, the last partial).
+    The gate is config 4's logsigmoid(randn - 2): with the mild gate of the shorter cases, one
+    bf16 rounding of the state that lands the other way in the kernel's fp32 summation order is
+    carried through 30 chunks, beyond the elementwise tolerance (1 of 5.2 M elements)."""
+    inp = _case(45 + K, B, T, H, K, K, shift=-2.0)
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
-@pytest.mark.parametrize("lens", [[1], [61, 3], [63, 64, 65], [1, 70, 128, 129], [5, 64, 129, 1023],
-                                  [127, 128, 129, 1, 2, 3, 300]])
-def test_varlen_cases(dev, lens):
+def test_varlen_fp32_balanced_order(dev):
+    """fp32 kernel with cu_seqlens and H % 8 == 0: the packed batch's XCD-balanced,
+    longest-first dispatch order, against the exact recurrence."""
+    lens = [300, 5, 129, 64, 1]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    inp = _case(40 + len(lens), 1, int(cu[-1]), 4, 64, 64, Hg=2, shift=4.0, cu=cu, profile="wy")
+    inp = _case(46, 1, int(cu[-1]), 8, 64, 64, dtype="f32", gate="linear", cu=cu)
+    out = abi_call(dev_inputs(inp, torch.float32, dev))
+    for name, got, ref in zip(("h", "v_new", "final"), out, O.fwd_h(**inp, compute_dtype=np.float64)):
+        assert_close(np32(got), ref, name=name, **F32_TOL)
+
+
+def test_varlen_balanced_order_with_helpers(dev):
+    """bf16 packed batch at H = 8 (the balanced order) with helper workgroups forced on: bit
+    identical to the run without helpers, and against the bf16 rounding model."""
+    lens = [700, 64, 1, 259]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(47, 1, int(cu[-1]), 8, 128, 128, Hg=4, shift=4.0, cu=cu, profile="wy")
+    d = dev_inputs(inp, torch.bfloat16, dev)
+    base = abi_call(d, tuning=dict(helpers=0, v_tile=32))
+    with_h = abi_call(d, tuning=dict(helpers=1, v_tile=32))
+    for a, b in zip(base, with_h):
+        assert torch.equal(a, b)
+    _check_bf16(with_h, inp)
+
+
+def test_varlen_many_short_sequences(dev):
+    """70 packed sequences at H = 8: more than the 64 lanes the kernel ranks sequences with, so
+    the dispatch keeps the natural order; against the bf16 rounding model."""
+    rng = np.random.default_rng(48)
+    lens = rng.integers(1, 200, 70)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(48, 1, int(cu[-1]), 8, 64, 64, Hg=8, shift=4.0, cu=cu, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
@@ -312,17 +373,19 @@ def test_headline_shape_parity(dev):
         assert torch.equal(x * 2, y)
 
 
-def test_partial_last_chunks_every_depth_deterministic(dev):
+@pytest.mark.parametrize("plan", PLANS, ids=PLAN_IDS)
+def test_partial_last_chunks_every_depth_deterministic(dev, plan):
     """Sequences of 1..5 chunks whose last chunk holds 1..64 rows, at every pipeline depth:
     the load wave's waits must cover a partial last chunk in flight (it issues fewer DMA
     instructions than a full one).  Repeated launches must be bit-identical."""
-    lens = [64 * j + r for j in range(5) for r in (1, 2, 17, 33, 63, 64)]
+    # 32 sequences at H = 1: 128 tasks of 16 columns or 64 of 32, so helpers fit beside them
+    lens = [64 * j + r for j in range(5) for r in (1, 2, 17, 33, 63, 64)] + [325, 7]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    inp = _case(80, 1, int(cu[-1]), 2, 64, 64, shift=4.0, cu=cu, profile="wy")
+    inp = _case(80, 1, int(cu[-1]), 1, 64, 64, shift=4.0, cu=cu, profile="wy")
     d = dev_inputs(inp, torch.bfloat16, dev)
     ref1 = O.fwd_h(**inp, rounding="bf16")
     for stages in (2, 3, 4):
-        outs = [abi_call(d, tuning=dict(stages=stages)) for _ in range(3)]
+        outs = [abi_call(d, tuning=dict(plan, stages=stages)) for _ in range(3)]
         for name, got, r in zip(("h", "v_new", "final"), outs[0], ref1):
             assert_close(np32(got), r, name=f"{name} stages={stages}", **BF16_TOL)
         for o in outs[1:]:
@@ -340,6 +403,8 @@ def test_partial_last_chunks_every_depth_deterministic(dev):
     (128, 128, 4, 4, dict(v_tile=32, helpers=1, load_waves=1)),
     (128, 128, 3, 1, dict(v_tile=64)),
     (256, 256, 2, 1, {}),
+    (96, 96, 3, 2, {}),                              # zero-padded key dims
+    (160, 160, 2, 1, {}),
 ])
 def test_o1_rounding_points_bit_exact(dev, K, V, n_chunks, H, env):
     """One-hot W and K rows make every contraction a single product, exact in any order, so
