@@ -29,6 +29,7 @@ CGDR_NUMERICS_CONTEST = 1
 EXPORTED_SYMBOLS = (
     "cgdr_fwd_h_workspace_size",
     "cgdr_fwd_h_launch",
+    "cgdr_fwd_h_launch_no_alloc",
     "cgdr_fwd_h_get_plan",
     "cgdr_prepare_chunk_offsets",
     "cgdr_prepare_chunk_indices",
@@ -223,6 +224,8 @@ def load(path: str | None = None):
     lib.cgdr_fwd_h_workspace_size.restype = ctypes.c_int
     lib.cgdr_fwd_h_launch.argtypes = [ctypes.POINTER(FwdHArgs), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.cgdr_fwd_h_launch.restype = ctypes.c_int
+    lib.cgdr_fwd_h_launch_no_alloc.argtypes = [ctypes.POINTER(FwdHArgs), ctypes.c_void_p]
+    lib.cgdr_fwd_h_launch_no_alloc.restype = ctypes.c_int
     lib.cgdr_fwd_h_get_plan.argtypes = [ctypes.POINTER(FwdHArgs), ctypes.POINTER(FwdHPlan)]
     lib.cgdr_fwd_h_get_plan.restype = ctypes.c_int
     lib.cgdr_prepare_chunk_offsets.argtypes = [_c_i64_p, ctypes.c_int64, ctypes.c_int64, _c_i64_p]
@@ -280,6 +283,15 @@ def launch(args: FwdHArgs, stream: int, workspace: int = 0, workspace_bytes: int
     that stays untouched by the caller until the launch has completed on that stream."""
     check(load().cgdr_fwd_h_launch(ctypes.byref(args), ctypes.c_void_p(workspace or None),
                                    ctypes.c_size_t(workspace_bytes), ctypes.c_void_p(stream)))
+
+
+NO_ALLOC_SCRATCH_BYTES = 16 << 20   # CGDR_NO_ALLOC_SCRATCH_BYTES
+
+
+def launch_no_alloc(args: FwdHArgs, stream: int) -> None:
+    """Enqueue on `stream` with the library's static per-GPU scratch instead of a workspace
+    (no device allocation); launches that overlap on one GPU race on that scratch."""
+    check(load().cgdr_fwd_h_launch_no_alloc(ctypes.byref(args), ctypes.c_void_p(stream)))
 
 
 def chunk_o_launch(args: ChunkOArgs, stream: int) -> None:

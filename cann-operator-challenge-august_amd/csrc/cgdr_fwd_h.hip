@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 
 #include "cgdr_fwd_h_dispatch.h"
 #include "cgdr_host.h"
@@ -385,6 +386,42 @@ hipError_t launch_g_relayout(const cgdr_fwd_h_args* a, float* gt, hipStream_t s)
   return hipGetLastError();
 }
 
+// Scratch of cgdr_fwd_h_launch_no_alloc: a file-scope device array that every GPU the library
+// runs on holds (its own copy, at its own address) until the process ends.  Host code never
+// passes the array's name to a kernel or a copy: its device address is looked up once per
+// device with hipGetSymbolAddress (scratch_address below) and that pointer is used instead.
+constexpr size_t kNoAllocScratchBytes = CGDR_NO_ALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on `device`, looked up on the first call for that device with
+// that device current (the caller's current device is restored afterwards).
+cgdr_status scratch_address(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(CGDR_ERR_UNSUPPORTED, "device %d is beyond the %d devices the static scratch serves", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] == nullptr) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+    if (cur != device && (e = hipSetDevice(device)) != hipSuccess)
+      return fail(CGDR_ERR_LAUNCH, "hipSetDevice(%d) failed: %s", device, hipGetErrorString(e));
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != device) (void)hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(CGDR_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                  hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return CGDR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -509,6 +546,26 @@ cgdr_status cgdr_prepare_chunk_indices(const int64_t* cu_seqlens, int64_t n_seq,
   }
   *nt_out = rows;
   return CGDR_OK;
+}
+
+cgdr_status cgdr_fwd_h_launch_no_alloc(const cgdr_fwd_h_args* args, void* stream) {
+  Plan pl;
+  cgdr_status st = make_plan(args, &pl);
+  if (st != CGDR_OK) return st;
+  const size_t need = workspace_bytes_of(args, pl);
+  if (need > kNoAllocScratchBytes)
+    return fail(CGDR_ERR_UNSUPPORTED,
+                "this call needs %zu bytes of scratch; cgdr_fwd_h_launch_no_alloc holds %zu (pass g with token "
+                "stride 1, or call cgdr_fwd_h_launch with a workspace)",
+                need, kNoAllocScratchBytes);
+  if (need == 0) return cgdr_fwd_h_launch(args, nullptr, 0, stream);
+  int device = -1;
+  hipError_t e = stream != nullptr ? hipStreamGetDevice((hipStream_t)stream, &device) : hipGetDevice(&device);
+  if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "cannot find the stream's device: %s", hipGetErrorString(e));
+  void* ws = nullptr;
+  st = scratch_address(device, &ws);
+  if (st != CGDR_OK) return st;
+  return cgdr_fwd_h_launch(args, ws, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"

@@ -152,6 +152,18 @@ cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* works
 cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Phase 2 without a workspace and without allocating.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The same kernels as cgdr_fwd_h_launch, with the
+ * workspace in a static device array of CGDR_NO_ALLOC_SCRATCH_BYTES (16 MiB) that each GPU
+ * holds until the process ends; a call whose phase-1 workspace size exceeds it (a token-major
+ * g needs B*H*T*4 bytes) returns CGDR_ERR_UNSUPPORTED.  It calls no hipMalloc/hipFree; the
+ * first call on a device looks up the array's address there.  Every call on one GPU shares
+ * that GPU's array: calls whose executions overlap on one GPU (other streams, or the same
+ * stream from several host threads without ordering) race on it. */
+#define CGDR_NO_ALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+cgdr_status cgdr_fwd_h_launch_no_alloc(const cgdr_fwd_h_args* args, void* stream);
+
 /* Launch plan chosen for `args` (host only): the kernel variant and its grid.
  * Exposed for tests and benchmarks; the reference's counterpart is the tiling data
  * written by ChunkGatedDeltaRuleFwdHTilingFunc (code/op_host/chunk_gated_delta_rule_fwd_h_tiling.cpp:152-261). */

@@ -29,9 +29,11 @@ _DT = {torch.bfloat16: _abi.CGDR_BF16, torch.float32: _abi.CGDR_F32}
 
 
 def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=torch.float32,
-             canary=float("nan"), tuning: dict | None = None):
+             canary=float("nan"), tuning: dict | None = None, numerics: int = 0, no_alloc: bool = False):
     """Token-major FwdH through the C ABI into output buffers pre-filled with `canary`;
-    `tuning` (fields of cgdr_fwd_h_tuning) overrides the launch plan."""
+    `tuning` (fields of cgdr_fwd_h_tuning) overrides the launch plan; `numerics` is a
+    cgdr_numerics; `no_alloc` calls cgdr_fwd_h_launch_no_alloc (its static scratch) instead of
+    cgdr_fwd_h_launch with a workspace."""
     k, w, u, g, h0, cu = d["k"], d["w"], d["u"], d["g"], d["initial_state"], d["cu_seqlens"]
     B, T, Hg, K = k.shape
     H, V = u.shape[2], u.shape[3]
@@ -72,9 +74,14 @@ def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=
         a.stride_h0[:] = list(h0.stride()[:2])
     if f is not None:
         a.stride_final[:] = list(f.stride()[:2])
+    a.numerics = numerics
     if tuning:
         t = _abi.make_tuning(**tuning)
         a.tuning = ctypes.pointer(t)
+    if no_alloc:
+        _abi.launch_no_alloc(a, torch.cuda.current_stream(k.device).cuda_stream)
+        torch.cuda.synchronize()
+        return h, v, f
     nws = _abi.workspace_size(a)
     ws = torch.full((max(nws, 1),), 0xAB, dtype=torch.uint8, device=k.device)
     _abi.launch(a, torch.cuda.current_stream(k.device).cuda_stream, ws.data_ptr() if nws else 0, nws)

@@ -1,0 +1,71 @@
+"""cgdr_fwd_h_launch_no_alloc (the entry point that allocates nothing: its workspace is a static
+per-GPU device array) against cgdr_fwd_h_launch with a caller-allocated workspace, bit for bit.
+
+Two calls in a row, the second smaller, so the second starts from what the first left in the
+shared scratch: token-major g (the head-major relayout of g lives in the scratch), helper
+workgroups (their progress counters), and contest numerics (the per-head redo flags).  The
+oversize rejection is checked on the host, before anything touches a GPU."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from cgdr_amd import _abi
+from gpu_util import abi_call, dev_inputs
+from oracle import cgdr_oracle as O
+
+
+def _inp(seed, T, H, K=128, V=128, cu=None):
+    print(f"[no_alloc] seed={seed} T={T} H={H} K={K} V={V} varlen={cu is not None}", flush=True)
+    return O.make_inputs(seed, 1, T, H, K, V, gate="logsigmoid", gate_shift=4.0, with_h0=True, cu_seqlens=cu,
+                         profile="wy")
+
+
+def _same(a, b):
+    for x, y in zip(a, b):
+        if x is None:
+            assert y is None
+            continue
+        assert torch.equal(x.view(torch.int16) if x.dtype == torch.bfloat16 else x.view(torch.int32),
+                           y.view(torch.int16) if y.dtype == torch.bfloat16 else y.view(torch.int32))
+
+
+@pytest.mark.gpu
+def test_no_alloc_matches_workspace_launch(dev):
+    # call 1: 8 heads x 4 V-tiles of 32 columns with helpers (progress counters), token-major g
+    # (its relayout: 256 KiB of the scratch); call 2: a smaller packed batch in contest numerics
+    cases = [(_inp(1, 8192, 8), dict(helpers=1, v_tile=32), 0),
+             (_inp(2, 1000, 4, cu=np.array([0, 300, 301, 1000], np.int64)), None, 1)]
+    for inp, tuning, numerics in cases:
+        d = dev_inputs(inp, torch.bfloat16, dev)
+        assert d["g"].stride(1) != 1   # token-major g: the workspace holds its relayout
+        ref = abi_call(d, tuning=tuning, numerics=numerics)
+        got = abi_call(d, tuning=tuning, numerics=numerics, no_alloc=True)
+        _same(ref, got)
+        again = abi_call(d, tuning=tuning, numerics=numerics, no_alloc=True)
+        _same(ref, again)
+
+
+def test_no_alloc_rejects_oversize_scratch():
+    """A token-major g of B*H*T*4 bytes beyond the 16 MiB scratch is refused with a message,
+    before any device call (no GPU needed)."""
+    a = _abi.FwdHArgs()
+    fake = 1 << 24
+    a.k = a.w = a.u = a.h = a.g = fake
+    B, T, H, K, V = 1, 1 << 17, 64, 64, 64          # g relayout: 32 MiB
+    a.B, a.T, a.H, a.Hg, a.K, a.V, a.N, a.NT = B, T, H, H, K, V, B, T // 64
+    a.chunk_size = 64
+    a.in_dtype = _abi.CGDR_BF16
+    a.stride_k[:] = [T * H * K, H * K, K]
+    a.stride_w[:] = [T * H * K, H * K, K]
+    a.stride_u[:] = [T * H * V, H * V, V]
+    a.stride_g[:] = [T * H, H, 1]
+    a.stride_h[:] = [(T // 64) * H * K * V, H * K * V, K * V]
+    n = ctypes.c_size_t(0)
+    assert _abi.load().cgdr_fwd_h_workspace_size(ctypes.byref(a), ctypes.byref(n)) == _abi.CGDR_OK
+    assert n.value > _abi.NO_ALLOC_SCRATCH_BYTES
+    st = _abi.load().cgdr_fwd_h_launch_no_alloc(ctypes.byref(a), None)
+    assert st == _abi.CGDR_ERR_UNSUPPORTED
+    assert "scratch" in _abi.last_error()
