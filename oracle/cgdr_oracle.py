@@ -30,6 +30,14 @@ What it restates (paths relative to the reference's
   ``docs/problem.txt:81-167``): bf16 state, bf16 GEMM outputs, saturating fp16 casts
   (``cast_to_float16``, ``generate_golden.py:285-290``) and ``nan_to_num`` after each GEMM.
   Pinned by the reference's own golden cases (``tests/golden/cases``).
+* ``fwd_h_bf16_state`` -- the reference's bf16 benchmark ``stage2_opt``
+  (``ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_benchmark.py:96-142``, key
+  gating from ``stage1_opt`` ``:74,83``): the state is rounded to bf16 after every chunk,
+  the gate scales k instead of v_new, every GEMM output is rounded to bf16.  It is the
+  "benchmark" side of the reference's three-way accuracy gate
+  (``ref/chunk_gated_delta_rule/tests/assets/impl/compare.py:32-35,93-196``).  Pinned by
+  vectors the reference's own ``stage1_opt``/``stage2_opt`` wrote
+  (``tests/golden/bf16_state``, ``tests/golden/make_bf16_state_golden.py``).
 * ``prepare_chunk_offsets`` / ``prepare_chunk_indices`` -- ``docs/problem.txt:251-270``
   and ``code/tests/golden/generate_golden.py:260-282``.
 * ``safe_exp`` -- ``docs/problem.txt:272-274``.
@@ -260,6 +268,73 @@ def fwd_h(
                 S = rnd(S)
         if output_final_state:
             final[n] = S
+    return h_out, v_out, final
+
+
+# ----------------------------------------------------------------------------- bf16-state benchmark
+
+def fwd_h_bf16_state(
+    k: np.ndarray,
+    w: np.ndarray,
+    u: np.ndarray,
+    g: np.ndarray | None = None,
+    initial_state: np.ndarray | None = None,
+    cu_seqlens: np.ndarray | None = None,
+    chunk_size: int = CHUNK_SIZE,
+):
+    """The reference's bf16 benchmark of the state recurrence, ``stage2_opt``
+    (``ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_benchmark.py:96-142``) with
+    the key gating of its ``stage1_opt`` (``:74``, ``:83``), written against the FwdH inputs
+    (``k_cumdecay = -w``, ``v_inner = u``, ``g_cum = g``) in the token-major layouts of
+    ``fwd_h``.  Per chunk, with S the state entering it (the initial state as given, bf16
+    values from the first chunk on):
+
+      v_new = bf16(u + bf16(-(w @ S)))                      (:130-131, bf16 + bf16 in bf16)
+      kg    = bf16(k * exp(g_last - g))                     (stage1 :74, :83; no clamp)
+      S     = bf16(bf16(S * exp(g_last)) + bf16(kg^T @ v_new))   (:133-136)
+
+    Every product is rounded once to bf16 (the benchmark's float32 accumulations, here taken
+    in float64, then rounded to float32 and to bf16).  ``h[c]`` (which the benchmark
+    does not return) is taken as bf16 of the state entering chunk c, the FwdH output's
+    definition.  Returns ``(h, v_new, final)`` as float32 arrays of bf16 values; the reference
+    keeps the benchmark's transposed ``[V, K]`` state, this keeps ``[K, V]``."""
+    if chunk_size != CHUNK_SIZE:
+        raise ValueError(f"chunk_size must be {CHUNK_SIZE}, got {chunk_size}")
+    f32 = np.float32
+    k = np.asarray(k, f32)
+    w = np.asarray(w, f32)
+    u = np.asarray(u, f32)
+    B, T, Hg, K = k.shape
+    H, V = u.shape[2], u.shape[3]
+    head_of_key = np.arange(H) // (H // Hg)
+    gq = None if g is None else np.asarray(g, f32)
+    seqs, NT = sequence_bounds(B, T, cu_seqlens, chunk_size)
+    h_out = np.zeros((B, NT, H, K, V), f32)
+    v_out = np.zeros((B, T, H, V), f32)
+    final = np.zeros((len(seqs), H, K, V), f32)
+    h0 = None if initial_state is None else np.asarray(initial_state, f32)
+    for n, (b, bos, eos, boh, _) in enumerate(seqs):
+        S = np.zeros((H, K, V), f32) if h0 is None else h0[n].copy()
+        for c, t0 in enumerate(range(bos, eos, chunk_size)):
+            t1 = min(t0 + chunk_size, eos)
+            h_out[b, boh + c] = bf16_round(S)
+            Kc = np.transpose(k[b, t0:t1][:, head_of_key, :], (1, 0, 2))   # [H, L, K]
+            Wc = np.transpose(w[b, t0:t1], (1, 0, 2))
+            Uc = np.transpose(u[b, t0:t1], (1, 0, 2))
+            vp = bf16_round(np.matmul(-Wc.astype(np.float64), S).astype(f32))
+            vn = bf16_round((Uc + vp).astype(f32))
+            v_out[b, t0:t1] = np.transpose(vn, (1, 0, 2))
+            if gq is not None:
+                gc = np.transpose(gq[b, t0:t1], (1, 0))                     # [H, L]
+                g_last = gc[:, -1]
+                kg = bf16_round((Kc * np.exp((g_last[:, None] - gc).astype(f32))[:, :, None]).astype(f32))
+                decay = np.exp(g_last).astype(f32)[:, None, None]
+            else:
+                kg = Kc
+                decay = f32(1.0)
+            upd = bf16_round(np.matmul(np.transpose(kg, (0, 2, 1)).astype(np.float64), vn).astype(f32))
+            S = bf16_round((bf16_round((S * decay).astype(f32)) + upd).astype(f32))
+        final[n] = S
     return h_out, v_out, final
 
 

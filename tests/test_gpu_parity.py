@@ -10,6 +10,9 @@ Tolerances (written per test):
     and elementwise rtol=2e-2, atol=2e-3 for inputs made by the WY producer, whose
     transitions contract as in a real Gated DeltaNet layer (at most a 1e-5 fraction of tail
     elements outside; the rounding model alone reaches 0.9 of the bound there).
+  * configs 1-4 (full size): the reference's own three-way gate (compare.py:32-35,93-196):
+    against the exact recurrence, the kernel's errors within 5x (max relative), 1.5x (mean
+    relative), 1.5x (RMSE) and 2x (small values) of the bf16-state benchmark's (stage2_opt).
 Bit-exact identities: V-tile and pipeline-depth invariance, varlen = separate sequences,
 GQA = repeated keys, exact linearity, head-major = token-major.
 """
@@ -20,6 +23,7 @@ import numpy as np
 import pytest
 import torch
 
+import accuracy_gate
 import cgdr_amd
 import o1_probe
 from gpu_util import abi_call, assert_close, assert_scale_close, dev_inputs, np32
@@ -47,6 +51,23 @@ def _check_bf16(d_out, inp, exact_frac=1e-2, names=("h", "v_new", "final"), exac
             # 1e-5 fraction of tail elements beyond it
             bad = np.abs(got - r3) > BF16_TOL["atol"] + BF16_TOL["rtol"] * np.abs(r3)
             assert bad.mean() <= 1e-5, f"{name} vs exact: {bad.sum()}/{bad.size} outside rtol=2e-2, atol=2e-3"
+    return ref3
+
+
+def _three_way(out, inp, ref3):
+    """The reference's own bf16 accuracy gate (compare.py:32-35,93-196, tests/accuracy_gate.py):
+    against the exact recurrence, the kernel's max and mean relative errors, RMSE and
+    small-value misses stay below 5x, 1.5x, 1.5x and 2x those of the reference's bf16-state
+    benchmark (stage2_opt, oracle.fwd_h_bf16_state) on the same inputs."""
+    bench = O.fwd_h_bf16_state(inp["k"], inp["w"], inp["u"], inp["g"], inp["initial_state"],
+                               cu_seqlens=inp["cu_seqlens"])
+    for name, got, g3, b in zip(("h", "v_new", "final"), out, ref3, bench):
+        if got is None:
+            continue
+        r = accuracy_gate.cross_check(got if isinstance(got, np.ndarray) else np32(got), g3, b)
+        print(f"  gate {name}: " + ", ".join(f"{k} {v:.3f}" for k, v in r["ratios"].items())
+              + f" (kernel max_re {r['npu']['max_re']:.3e}, benchmark {r['bench']['max_re']:.3e})", flush=True)
+        assert r["passed"], (name, r)
 
 
 def _case(seed, B, T, H, K, V, Hg=None, dtype="bf16", gate="logsigmoid", shift=0.0, h0=True, cu=None,
@@ -72,7 +93,8 @@ def test_config0_fp32(dev, gate):
 
 def test_config1_bf16(dev):
     inp = _case(1, 2, 2048, 16, 128, 128)
-    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
+    out = abi_call(dev_inputs(inp, torch.bfloat16, dev))
+    _three_way(out, inp, _check_bf16(out, inp))
 
 
 def test_config1_bf16_mild_decay_wy(dev):
@@ -105,16 +127,18 @@ def test_config3_varlen_full_size(dev):
     sub = dict(inp, k=inp["k"][:, :, heads], w=inp["w"][:, :, heads], u=inp["u"][:, :, heads],
                g=inp["g"][:, :, heads], initial_state=inp["initial_state"][:, heads])
     ref3 = O.fwd_h(**sub)
-    for name, got, r3, ax in zip(("h", "v_new", "final"), out, ref3, (2, 2, 1)):
-        got = np.take(got, np.arange(32)[heads], axis=ax)
+    sub_out = [np.take(got, np.arange(32)[heads], axis=ax) for got, ax in zip(out, (2, 2, 1))]
+    for name, got, r3 in zip(("h", "v_new", "final"), sub_out, ref3):
         assert_scale_close(got, r3, 1e-2, name=f"{name} vs exact")
+    _three_way(sub_out, sub, ref3)
 
 
 def test_config4_full_size(dev):
     """Config 4 at its full size: B=4, T=8192, H=8, K=128, V=256, g the chunk-local cumsum of
     logsigmoid(randn - 2), so exp(g) spans ~1e-30 .. 1."""
     inp = _case(41, 4, 8192, 8, 128, 256, shift=-2.0)
-    _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
+    out = abi_call(dev_inputs(inp, torch.bfloat16, dev))
+    _three_way(out, inp, _check_bf16(out, inp))
 
 
 # ---------------------------------------------------------------- shapes and edge cases
@@ -363,9 +387,11 @@ def test_headline_shape_parity(dev):
     outs = [np32(x) for x in out]
     for name, got, r in zip(("h", "v_new", "final"), outs, O.fwd_h(**inp, rounding="bf16")):
         assert_close(got, r, name=f"{name} vs bf16 model", **BF16_TOL)
-    for name, got, r in zip(("h", "v_new", "final"), outs, O.fwd_h(**inp)):
+    ref3 = O.fwd_h(**inp)
+    for name, got, r in zip(("h", "v_new", "final"), outs, ref3):
         assert_scale_close(got, r, 1e-2, name=name)
-    del outs
+    _three_way(outs, inp, ref3)
+    del outs, ref3
     # exact linearity at full size
     d2 = dict(d, u=d["u"] * 2)
     out2 = abi_call(d2)

@@ -11,6 +11,9 @@ The chunked recurrence is checked against things that do not share its code:
   * torch's float->bfloat16 conversion for the rounding helper.
 """
 
+import glob
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -252,3 +255,76 @@ def test_o1_probe_distinguishes_each_rule():
     assert np.array_equal(final[0, 0, :16], h0[0, 0, :16])          # fp32 state carried
     u0 = inp["u"][0, 16:32, 0]
     assert not np.array_equal(v_new[0, 16:32, 0], O.bf16_round(u0 - h0[0, 0, :16]))
+
+
+# ----------------------------------------------------------------------------- bf16-state benchmark
+
+BF16_STATE_CASES = sorted(os.path.basename(f)[:-4] for f in glob.glob(os.path.join(
+    os.path.dirname(__file__), "golden", "bf16_state", "*.npz")))
+
+
+def _bf16_state_case(name):
+    a = np.load(os.path.join(os.path.dirname(__file__), "golden", "bf16_state", name + ".npz"))
+    cu = a["cu_seqlens"] if len(a["cu_seqlens"]) > 2 else None
+    return a, cu
+
+
+@pytest.mark.parametrize("name", BF16_STATE_CASES)
+def test_bf16_state_oracle_matches_reference_vectors(name):
+    """fwd_h_bf16_state against the vectors the reference's own stage1_opt/stage2_opt wrote
+    (tests/golden/make_bf16_state_golden.py): v_new bit for bit; the final state bit for bit
+    but for a float32 accumulation-order residue of at most one bf16 ulp (1 of 1,024
+    elements on the 10-chunk case)."""
+    a, cu = _bf16_state_case(name)
+    _, v, fin = O.fwd_h_bf16_state(a["k"], a["w"], a["u"], a["g"], a["h0"], cu_seqlens=cu)
+    assert np.array_equal(v, a["v_new"]), name
+    assert (fin == a["final"]).mean() >= 0.998, name
+    ulp = np.abs(a["final"]) * 2.0 ** -7 + 1e-30
+    assert (np.abs(fin - a["final"]) <= ulp).all(), name
+
+
+@pytest.mark.parametrize("name", BF16_STATE_CASES)
+def test_bf16_state_vectors_tell_the_rounding_models_apart(name):
+    """The same vectors reject the other rounding models: the Triton kernel's (fp32 state,
+    gate on v_new) and the exact recurrence both miss v_new or the final state, so the
+    fixtures pin where the benchmark rounds, not only its scale."""
+    a, cu = _bf16_state_case(name)
+    for rounding in ("bf16", None):
+        _, v, fin = O.fwd_h(a["k"], a["w"], a["u"], a["g"], a["h0"], cu_seqlens=cu, rounding=rounding)
+        v = O.bf16_round(v)
+        fin = O.bf16_round(fin)
+        assert (v != a["v_new"]).any() or (fin != a["final"]).mean() > 0.01, (name, rounding)
+
+
+def test_accuracy_gate_restatement():
+    """tests/accuracy_gate.py follows compare.py's rules (compare.py:32-35,55-196): equal
+    outputs pass; a device whose max relative error is 6x the benchmark's fails on that ratio
+    alone; errors below 2^-7 pass whatever the ratio; the benchmark's errors are floored at
+    2^-8; a small golden value the device misses counts in smra."""
+    import accuracy_gate as G
+    rng = np.random.default_rng(0)
+    g = rng.uniform(0.5, 1.0, 4096).astype(np.float32)
+    assert G.cross_check(g, g, g)["passed"]
+    bench = g.copy()
+    bench[0] += 0.05 * (g[0] + 1e-3)              # benchmark max_re 0.05
+    npu = g.copy()
+    npu[1] += 0.30 * (g[1] + 1e-3)                # device max_re 0.30 = 6x, mean and rmse tiny
+    r = G.cross_check(npu, g, bench)
+    assert not r["passed"] and r["ratios"]["max_re"] == pytest.approx(6.0, rel=1e-3)
+    assert r["ratios"]["avg_re"] < 1.5 and r["ratios"]["rmse"] < 1.5
+    npu = g.copy()
+    npu[1] += 0.006 * (g[1] + 1e-3)               # below 2^-7: passes although 6x a tiny bench
+    tiny = g.copy()
+    tiny[0] += 0.001 * (g[0] + 1e-3)
+    assert G.cross_check(npu, g, tiny)["passed"]
+    # a benchmark error below 2^-8 counts as 2^-8, so a device max_re of 4 * 2^-8 passes;
+    # against an exact benchmark any device error is an infinite ratio
+    npu = g.copy()
+    npu[2] += 4 * 2.0 ** -8 * (g[2] + 1e-3)
+    r = G.cross_check(npu, g, tiny)
+    assert r["ratios"]["max_re"] == pytest.approx(4.0, rel=1e-3) and r["passed"]
+    r = G.cross_check(npu, g, g)
+    assert r["ratios"]["max_re"] == float("inf") and not r["passed"]
+    # small golden values (|g| < 2^-10): 3 of 4 missed
+    gs = np.full(4, 2.0 ** -12, np.float32)
+    assert G.errors(gs + np.array([0, 1e-5, 1e-5, 1e-5], np.float32), gs)["smra"] == pytest.approx(0.75)
