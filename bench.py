@@ -79,6 +79,11 @@ FWD_H_WORKLOADS = {
                    B=1, T=None, H=32, Hg=32, K=128, V=128, h0=True, shift=0.0, n_seq=16),
     "wide_v": dict(desc="ChunkGatedDeltaRuleFwdH wide value heads, gate logsigmoid(randn-2)", B=4, T=8192, H=8,
                    Hg=8, K=128, V=256, h0=True, shift=-2.0),
+    # the fp32 kernel (fp32 k/w/u/h/v_new): the CPU-runnable reference case and config 1's shape
+    "config0_fp32": dict(desc="ChunkGatedDeltaRuleFwdH fp32, the CPU-runnable case", B=1, T=256, H=2, Hg=2, K=64,
+                         V=64, h0=True, shift=0.0, dtype="f32"),
+    "config1_fp32": dict(desc="ChunkGatedDeltaRuleFwdH fp32 at B=2, T=2048, H=16, K=V=128", B=2, T=2048, H=16,
+                         Hg=16, K=128, V=128, h0=True, shift=0.0, dtype="f32"),
 }
 
 
@@ -113,7 +118,8 @@ def make_workload_inputs(torch, dev, name: str, seed: int = 0):
         x = torch.nn.functional.pad(inc[:, s:e], (0, 0, 0, pad)).view(B, -1, 64, H).cumsum(dim=2)
         g[:, s:e] = x.view(B, -1, H)[:, :L]
     h0 = torch.randn(N, H, K, V, generator=gen) * 0.1 if c["h0"] else None
-    t = dict(k=k.to(dev, torch.bfloat16), w=w.to(dev, torch.bfloat16), u=u.to(dev, torch.bfloat16),
+    dt = torch.float32 if c.get("dtype") == "f32" else torch.bfloat16
+    t = dict(k=k.to(dev, dt), w=w.to(dev, dt), u=u.to(dev, dt),
              g=g.to(dev).transpose(1, 2).contiguous().transpose(1, 2),
              initial_state=None if h0 is None else h0.to(dev), cu_seqlens=cu)
     return t, dict(B=B, T=T, H=H, Hg=Hg, K=K, V=V, N=N, NT=NT, chunk_size=64)
@@ -479,7 +485,8 @@ def main():
     avg_ms = sum(kern_ms) / len(kern_ms)
     progress(f"timed {args.steps} fwd_h steps; per-step ms: " + " ".join(f"{x:.4f}" for x in kern_ms))
 
-    nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, N, h0_bytes=4 if h0 is not None else 0)
+    es = k.element_size()
+    nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, N, s_in=es, s_out=es, h0_bytes=4 if h0 is not None else 0)
     flops = algorithmic_flops(B, NT, H, K, V)
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = B * T * args.steps / wall
@@ -505,7 +512,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "f32" if es == 4 else "bf16",
         "data": "synthetic",
         "config": {"workload": FWD_H_WORKLOADS[args.workload]["desc"], **W,
                    "h0": "fp32 [N,H,K,V]" if h0 is not None else None, "output_final_state": True,

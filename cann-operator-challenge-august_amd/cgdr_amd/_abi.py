@@ -12,7 +12,7 @@ import ctypes
 import os
 
 CHUNK_SIZE = 64
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CGDR_OK = 0
 CGDR_ERR_NULLPTR = 1
@@ -25,6 +25,9 @@ CGDR_F32 = 1
 
 CGDR_NUMERICS_DEFAULT = 0
 CGDR_NUMERICS_CONTEST = 1
+
+CGDR_STATE_KV = 0
+CGDR_STATE_VK = 1
 
 EXPORTED_SYMBOLS = (
     "cgdr_fwd_h_workspace_size",
@@ -111,6 +114,8 @@ class FwdHArgs(ctypes.Structure):
         ("stride_h0", ctypes.c_int64 * 2),
         ("stride_final", ctypes.c_int64 * 2),
         ("tuning", ctypes.POINTER(FwdHTuning)),
+        ("state_layout", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
     ]
 
 

@@ -33,6 +33,7 @@ _DTYPES = {torch.bfloat16: _abi.CGDR_BF16, torch.float32: _abi.CGDR_F32}
 # exact fp32 for fp32 inputs; "contest": the contest reference run()'s fp16-saturating,
 # bf16-state numerics (docs/problem.txt:81-167), bf16 inputs only.
 _NUMERICS = {"default": _abi.CGDR_NUMERICS_DEFAULT, "contest": _abi.CGDR_NUMERICS_CONTEST}
+_STATE_LAYOUTS = {"kv": _abi.CGDR_STATE_KV, "vk": _abi.CGDR_STATE_VK}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -84,8 +85,10 @@ def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets,
 
 
 def _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT,
-            strides: dict, numerics: str = "default", tuning: dict | None = None) -> None:
+            strides: dict, numerics: str = "default", tuning: dict | None = None,
+            state_layout: str = "kv") -> None:
     a = _abi.FwdHArgs()
+    a.state_layout = _STATE_LAYOUTS[state_layout]
     if tuning:
         t = _abi.make_tuning(**tuning)
         a.tuning = ctypes.pointer(t)
@@ -149,8 +152,13 @@ def chunk_gated_delta_rule_fwd_h(
     final_state_dtype: torch.dtype = torch.float32,
     numerics: str = "default",
     tuning: dict | None = None,
+    state_layout: str = "kv",
 ):
     """``(h, v_new, final_state)`` for token-major inputs; see the module docstring.
+    ``state_layout="vk"`` takes ``initial_state`` and returns ``final_state`` as ``[N,H,V,K]``
+    blocks (the full operator's ``[B,Nv,Dv,Dk]`` state,
+    ``ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_benchmark.py:184``); h stays
+    ``[B,NT,H,K,V]``.
     ``numerics="contest"`` selects the contest reference's rounding model (bf16 inputs).
     ``tuning`` overrides fields of the launch plan (``cgdr_fwd_h_tuning``: v_tile, helpers,
     load_waves, stages, ...); outputs do not depend on it.
@@ -159,6 +167,8 @@ def chunk_gated_delta_rule_fwd_h(
     initial_state in fp32 or bf16 (other dtypes are upcast to fp32).
     """
     _check_common(k, w, u, g, initial_state, chunk_size)
+    if state_layout not in _STATE_LAYOUTS:
+        raise ValueError(f"state_layout must be one of {sorted(_STATE_LAYOUTS)}, got {state_layout!r}")
     B, T, Hg, K = k.shape
     H, V = u.shape[-2], u.shape[-1]
     if tuple(w.shape) != (B, T, H, K):
@@ -184,16 +194,18 @@ def chunk_gated_delta_rule_fwd_h(
         N, NT, cu_dev, offs_dev = _varlen_meta(cu_seqlens, T, chunk_indices, chunk_offsets, dev)
     h0 = None
     if initial_state is not None:
-        if tuple(initial_state.shape) != (N, H, K, V):
-            raise ValueError(f"initial_state must have shape [N,H,K,V]={[N, H, K, V]}, got {list(initial_state.shape)}")
+        want = (N, H, K, V) if state_layout == "kv" else (N, H, V, K)
+        if tuple(initial_state.shape) != want:
+            raise ValueError(f"initial_state must have shape {list(want)} ({state_layout}), got {list(initial_state.shape)}")
         h0 = initial_state if initial_state.dtype in _DTYPES else initial_state.float()
         h0 = h0.contiguous()
-    align = 16 if k.dtype == torch.bfloat16 else 4
+    align = 16   # 16-byte rows: direct-to-LDS loads (bf16), vector loads (fp32)
     k, w, u = _prep_input(k, "k", align), _prep_input(w, "w", align), _prep_input(u, "u", align)
 
     h = k.new_empty(B, NT, H, K, V)
     v_new = torch.empty(B, T, H, V, dtype=u.dtype, device=dev) if save_new_value else None
-    final = (torch.empty(N, H, K, V, dtype=final_state_dtype, device=dev)
+    fshape = (N, H, K, V) if state_layout == "kv" else (N, H, V, K)
+    final = (torch.empty(*fshape, dtype=final_state_dtype, device=dev)
              if output_final_state else None)
     if final is not None and final.dtype not in _DTYPES:
         raise TypeError("final_state_dtype must be float32 or bfloat16")
@@ -205,7 +217,7 @@ def chunk_gated_delta_rule_fwd_h(
         stride_final=final.stride()[:2] if final is not None else None,
     )
     _launch(k, w, u, g, h0, cu_dev, offs_dev, h, v_new, final, B, T, H, Hg, K, V, N, NT, strides, numerics,
-            tuning)
+            tuning, state_layout)
     return h, v_new, final
 
 
@@ -240,7 +252,7 @@ def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_S
     if initial_state is not None:
         h0 = initial_state.reshape(N, H, K, V)
         h0 = (h0 if h0.dtype in _DTYPES else h0.float()).contiguous()
-    align = 16 if k.dtype == torch.bfloat16 else 4
+    align = 16   # 16-byte rows: direct-to-LDS loads (bf16), vector loads (fp32)
     k, w, u = _prep_input(k, "k", align), _prep_input(w, "w", align), _prep_input(u, "u", align)
     S = torch.empty(B, H, NT, K, V, dtype=k.dtype, device=dev)
     v = torch.empty(B, H, T, V, dtype=u.dtype, device=dev)

@@ -51,6 +51,9 @@ cgdr_status validate(const cgdr_fwd_h_args* a) {
     return fail(CGDR_ERR_INVALID, "numerics %d is not a cgdr_numerics", a->numerics);
   if (a->numerics == CGDR_NUMERICS_CONTEST && a->in_dtype != CGDR_BF16)
     return fail(CGDR_ERR_UNSUPPORTED, "contest numerics are defined for bf16 inputs only");
+  if (a->state_layout != CGDR_STATE_KV && a->state_layout != CGDR_STATE_VK)
+    return fail(CGDR_ERR_INVALID, "state_layout %d is not a cgdr_state_layout", a->state_layout);
+  if (a->reserved != 0) return fail(CGDR_ERR_INVALID, "reserved must be 0");
   if (a->B < 1) return fail(CGDR_ERR_INVALID, "B must be >= 1, but got %lld", (long long)a->B);
   if (a->T < 1) return fail(CGDR_ERR_INVALID, "T must be >= 1, but got %lld", (long long)a->T);
   if (a->H < 1 || a->Hg < 1)
@@ -151,8 +154,8 @@ int kernel_kd(int64_t K) { return K <= 32 ? 32 : K <= 64 ? 64 : K <= 128 ? 128 :
 
 // Kernel variant and grid.  The kernels need K a multiple of 16 (whole 16-row state tiles; the
 // reference accepts any K = V in [32, 256], _infershape.cpp:35-36,214-223), V a multiple of
-// 16, 16-byte aligned rows of k/w/u (direct-to-LDS loads move 16 bytes per lane) and 8-byte
-// aligned rows of h/v_new.
+// 16, 16-byte aligned rows of k/w/u (direct-to-LDS loads, and the fp32 kernel's vector loads,
+// move 16 bytes per lane) and 8-byte aligned rows of h/v_new.
 cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   cgdr_status st = validate(a);
   if (st != CGDR_OK) return st;
@@ -166,7 +169,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   const int kd = kernel_kd(K);
   if (V % 16 != 0)
     return fail(CGDR_ERR_UNSUPPORTED, "V=%lld is not supported (must be a multiple of 16)", (long long)V);
-  const int row_align = a->in_dtype == CGDR_BF16 ? 16 : 4;
+  const int row_align = 16;   // bf16: direct-to-LDS loads; fp32: 16-byte vector loads
   const void* ptrs[] = {a->k, a->w, a->u};
   const int64_t* strides[] = {a->stride_k, a->stride_w, a->stride_u};
   for (int i = 0; i < 3; ++i) {
@@ -224,7 +227,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     pl->ncw = ncw;
     pl->nlw = 0;
     pl->stages = 1;
-    pl->threads = 64 * ncw;
+    pl->threads = cgdr::F32Layout<32, 1>::THREADS;   // four waves at every key dim
   } else {
     // bf16: the pipelined kernel, with the contest rounding model when asked for
     pl->kernel = a->numerics == CGDR_NUMERICS_CONTEST ? 2 : 0;
@@ -294,6 +297,7 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   }
   p.n_xcd = pl.xcds;
   p.K = (int32_t)a->K;
+  p.state_vk = a->state_layout == CGDR_STATE_VK;
   p.progress = nullptr;
   return p;
 }

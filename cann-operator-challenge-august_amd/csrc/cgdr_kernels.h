@@ -106,6 +106,7 @@ struct FwdHParams {
   int32_t n_xcd;        // XCDs workgroups are dealt to round-robin (blockIdx % n_xcd)
   int32_t K;            // key dim, a multiple of 16 up to the kernel's KD: columns K..KD-1 of
                         // the K and W tiles and rows K..KD-1 of the state are zero padding
+  int32_t state_vk;     // initial and final state blocks are V x K (rows of K), else K x V
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
                         // task (kProgressStride ints; zeroed before launch)
   int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
@@ -547,7 +548,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-          const int64_t off = base + (int64_t)krow * p.V + vcol;
+          const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
           S[kt][r] = krow >= p.K ? 0.f
                      : p.h0_f32 ? ((const float*)p.h0)[off]
                                 : bf16_lo(((const unsigned short*)p.h0)[off]);
@@ -776,7 +777,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-          const int64_t off = base + (int64_t)krow * p.V + vcol;
+          const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
           if (krow >= p.K) continue;
           if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
           else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
@@ -1089,8 +1090,10 @@ static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __re
 // =============================================================================================
 // fp32 kernel (fp32 k/w/u/h/v_new): same task decomposition and the same tile orderings
 // (pi, sigma) with v_mfma_f32_16x16x4_f32, whose operands are one element per lane, so no
-// transposed reads are needed.  All waves load the next chunk with plain loads; it is the
-// exact-arithmetic path (fp32 products, fp32 accumulation) and is not the performance path.
+// transposed reads are needed.  Four waves per workgroup: waves 0 .. NCW-1 compute; all four
+// load chunk c+1 into registers (16-byte loads) while chunk c is computed, and store it to LDS
+// after the chunk's barrier.  It is the exact-arithmetic path (fp32 products, fp32
+// accumulation).
 // =============================================================================================
 
 template <int KD, int NCW>
@@ -1102,11 +1105,13 @@ struct F32Layout {
   static constexpr int U_OFF = 2 * 64 * WP * 4;
   static constexpr int G_OFF = U_OFF + 64 * (VT + 4) * 4;
   static constexpr int LDS_BYTES = G_OFF + 80 * 4;
-  static constexpr int THREADS = 64 * NCW;
+  static constexpr int THREADS = 256;                 // four waves load; NCW of them compute
+  static constexpr int PW = 64 * KD / 4 / THREADS;    // 16-byte pieces per thread of the W (and K) tile
+  static constexpr int PU = 64 * VT / 4 / THREADS;    // ... of the U tile
 };
 
 template <int KD, int NCW>
-__global__ void __launch_bounds__(64 * NCW)
+__global__ void __launch_bounds__(256)
 cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   using L = F32Layout<KD, NCW>;
   constexpr int VT = L::VT, WP = L::WP, UP = VT + 4;
@@ -1134,15 +1139,16 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   E* hb_ = (E*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h;
   E* vb_ = p.v_new == nullptr ? nullptr : (E*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h;
 
+  const bool computes = wave < NCW;   // uniform per wave
   f32x4 S[KT];
-  if (p.h0 != nullptr) {
+  if (computes && p.h0 != nullptr) {
     const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-        const int64_t off = base + (int64_t)krow * p.V + vcol;
+        const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
         S[kt][r] = krow >= p.K ? 0.f
                    : p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
       }
@@ -1151,25 +1157,56 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     for (int kt = 0; kt < KT; ++kt) S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // Chunk c's tiles in registers: thread i holds 16-byte pieces i, i + 256, ... of each tile
+  // (rows past the sequence end and key columns past K read as zero), and wave 0 the g row.
+  const int tid = threadIdx.x;
+  f32x4 rw[L::PW], rk[L::PW], ru[L::PU];
+  float rg = 0.f;
+  auto chunk_len = [&](int c) {
+    const int64_t rem = tk.len - (int64_t)c * kChunk;
+    return rem < kChunk ? (int)rem : kChunk;
+  };
+  auto fetch = [&](int c) {
+    const int64_t t0 = tk.bos + (int64_t)c * kChunk;
+    const int len = chunk_len(c);
+#pragma unroll
+    for (int i = 0; i < L::PW; ++i) {
+      const int q = tid + L::THREADS * i, r = q / (KD / 4), c4 = 4 * (q % (KD / 4));
+      const bool ok = r < len && c4 < p.K;
+      rw[i] = ok ? *(const f32x4*)(wb_ + (t0 + r) * p.sw_t + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      rk[i] = ok ? *(const f32x4*)(kb_ + (t0 + r) * p.sk_t + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < L::PU; ++i) {
+      const int q = tid + L::THREADS * i, r = q / (VT / 4), c4 = 4 * (q % (VT / 4));
+      ru[i] = r < len ? *(const f32x4*)(ub_ + (t0 + r) * p.su_t + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (tid < 64) rg = (gb_ != nullptr && tid < len) ? gb_[(t0 + tid) * p.sg_t] : 0.f;
+  };
+  // K = 256: the tiles of the next chunk and the state do not fit the registers together, so
+  // each chunk is loaded after its barrier instead of during the previous chunk
+  constexpr bool PREFETCH = KD <= 128;
+  if (PREFETCH && tk.nc > 0) fetch(0);
+
   for (int c = 0; c < tk.nc; ++c) {
     const int64_t t0 = tk.bos + (int64_t)c * kChunk;
-    const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
-    __syncthreads();
-    {
-      for (int idx = threadIdx.x; idx < 64 * KD; idx += L::THREADS) {
-        const int r = idx / KD, col = idx % KD;
-        const bool ok = r < len && col < p.K;   // zero rows past the end and padding columns
-        Ws[r * WP + col] = ok ? (float)wb_[(t0 + r) * p.sw_t + col] : 0.f;
-        Ks[r * WP + col] = ok ? (float)kb_[(t0 + r) * p.sk_t + col] : 0.f;
-      }
-      for (int idx = threadIdx.x; idx < 64 * VT; idx += L::THREADS) {
-        const int r = idx / VT, col = idx % VT;
-        Us[r * UP + col] = r < len ? (float)ub_[(t0 + r) * p.su_t + col] : 0.f;
-      }
+    const int len = chunk_len(c);
+    __syncthreads();   // the previous chunk's reads of the tiles are done
+    if constexpr (!PREFETCH) fetch(c);
+#pragma unroll
+    for (int i = 0; i < L::PW; ++i) {
+      const int q = tid + L::THREADS * i, r = q / (KD / 4), c4 = 4 * (q % (KD / 4));
+      *(f32x4*)(Ws + r * WP + c4) = rw[i];
+      *(f32x4*)(Ks + r * WP + c4) = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < L::PU; ++i) {
+      const int q = tid + L::THREADS * i, r = q / (VT / 4), c4 = 4 * (q % (VT / 4));
+      *(f32x4*)(Us + r * UP + c4) = ru[i];
     }
     if (threadIdx.x < 64) {
       const int t = threadIdx.x;
-      const float gv = (gb_ != nullptr && t < len) ? gb_[(t0 + t) * p.sg_t] : 0.f;
+      const float gv = rg;
       float gamma = t < len ? 1.f : 0.f, a = 1.f;
       if (gb_ != nullptr) {
         const float glast = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(gv), len - 1));
@@ -1180,6 +1217,8 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       if (t == 0) Gs[64] = a;
     }
     __syncthreads();
+    if (PREFETCH && c + 1 < tk.nc) fetch(c + 1);   // in flight while chunk c is computed
+    if (!computes) continue;
 
     // h snapshot (exact)
     {
@@ -1233,14 +1272,14 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
       S[kt] = up;
     }
   }
-  if (p.final_state != nullptr) {
+  if (computes && p.final_state != nullptr) {
     const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
 #pragma unroll
     for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-        const int64_t off = base + (int64_t)krow * p.V + vcol;
+        const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
         if (krow >= p.K) continue;
         if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
         else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];

@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define CGDR_ABI_VERSION 2
+#define CGDR_ABI_VERSION 3
 #define CGDR_CHUNK_SIZE 64
 
 /* Status codes.  The reference's aclnnStatus values for the same conditions are
@@ -97,6 +97,14 @@ typedef struct cgdr_fwd_h_tuning {
   int32_t reserved;      /* must be 0                                                          */
 } cgdr_fwd_h_tuning;
 
+/* Layout of each head's block in initial_state and final_state (h is always K x V). */
+typedef enum cgdr_state_layout {
+  CGDR_STATE_KV = 0,  /* K x V, rows of V: the Triton wrapper's [N,H,K,V] (docs/problem.txt:441-446) */
+  CGDR_STATE_VK = 1   /* V x K, rows of K: the full operator's [N,Nv,Dv,Dk]
+                         (ref/chunk_gated_delta_rule/tests/pytest/chunk_gated_delta_rule_benchmark.py:101,184;
+                         ref/chunk_gated_delta_rule/tests/assets/impl/golden.py:113-115) */
+} cgdr_state_layout;
+
 /* Arguments of one FwdH call.  Field meaning follows the Triton wrapper
  * (docs/problem.txt:436-472): k [B,T,Hg,K], w [B,T,H,K], u [B,T,H,V], g [B,T,H],
  * initial_state [N,H,K,V] -> h [B,NT,H,K,V], v_new [B,T,H,V], final_state [N,H,K,V]. */
@@ -133,6 +141,8 @@ typedef struct cgdr_fwd_h_args {
   int64_t stride_final[2];      /* (n, head); each K x V block contiguous                  */
 
   const cgdr_fwd_h_tuning* tuning; /* nullable (host memory): plan overrides, see above    */
+  int32_t state_layout;         /* cgdr_state_layout of initial_state and final_state     */
+  int32_t reserved;             /* must be 0                                              */
 } cgdr_fwd_h_args;
 
 /* Phase 1 (host only, no device access): validate the arguments and report the

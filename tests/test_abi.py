@@ -53,6 +53,7 @@ int main(void) {
   F(cgdr_fwd_h_args, final_state); F(cgdr_fwd_h_args, B); F(cgdr_fwd_h_args, chunk_size);
   F(cgdr_fwd_h_args, in_dtype); F(cgdr_fwd_h_args, numerics); F(cgdr_fwd_h_args, stride_k);
   F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final); F(cgdr_fwd_h_args, tuning);
+  F(cgdr_fwd_h_args, state_layout); F(cgdr_fwd_h_args, reserved);
   F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups); F(cgdr_fwd_h_plan, helpers);
   F(cgdr_fwd_h_plan, xcd_count);
   F(cgdr_fwd_h_tuning, helpers); F(cgdr_fwd_h_tuning, cu_count); F(cgdr_fwd_h_tuning, reserved);
@@ -174,6 +175,8 @@ def test_launch_rejects_missing_or_short_workspace(lib):
     (lambda a: setattr(a, "K", 16), _abi.CGDR_ERR_UNSUPPORTED),    # below 32
     (lambda a: setattr(a, "V", 24), _abi.CGDR_ERR_UNSUPPORTED),
     (lambda a: setattr(a, "in_dtype", 7), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "state_layout", 2), _abi.CGDR_ERR_INVALID),
+    (lambda a: setattr(a, "reserved", 1), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "k", (1 << 24) + 8), _abi.CGDR_ERR_UNSUPPORTED),   # DMA needs 16B rows
     (lambda a: setattr(a, "chunk_offsets", 1 << 24), _abi.CGDR_ERR_INVALID),  # without cu_seqlens
 ])

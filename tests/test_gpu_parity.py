@@ -251,6 +251,27 @@ def test_optional_outputs_and_dtypes(dev):
     assert torch.equal(h, h2)
 
 
+@pytest.mark.parametrize("dtype,K,V", [("bf16", 128, 128), ("bf16", 96, 64), ("f32", 64, 32)])
+def test_transposed_state_layout(dev, dtype, K, V):
+    """state_layout="vk": initial_state and final_state as [N,H,V,K] blocks (the full operator's
+    [B,Nv,Dv,Dk] state) give, bit for bit, the transposes of the [N,H,K,V] run, with packed
+    sequences, a padded key dim and the fp32 kernel."""
+    lens = [100, 64, 29]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(53, 1, int(cu[-1]), 4, K, V, Hg=2, dtype=dtype, gate="linear", cu=cu)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    d = dev_inputs(inp, tdt, dev)
+    kw = dict(g=d["g"], output_final_state=True, cu_seqlens=d["cu_seqlens"])
+    h, v, f = cgdr_amd.chunk_gated_delta_rule_fwd_h(d["k"], d["w"], d["u"], initial_state=d["initial_state"], **kw)
+    h0_vk = d["initial_state"].transpose(-1, -2).contiguous()
+    h2, v2, f2 = cgdr_amd.chunk_gated_delta_rule_fwd_h(d["k"], d["w"], d["u"], initial_state=h0_vk,
+                                                       state_layout="vk", **kw)
+    torch.cuda.synchronize()
+    assert tuple(f2.shape) == (len(lens), 4, V, K)
+    assert torch.equal(h, h2) and torch.equal(v, v2)
+    assert torch.equal(f.transpose(-1, -2), f2)
+
+
 def test_first_snapshot_is_initial_state(dev):
     inp = _case(52, 3, 100, 2, 128, 128, gate="linear")
     h, _, _ = abi_call(dev_inputs(inp, torch.bfloat16, dev))
@@ -268,6 +289,18 @@ def test_vtile_and_depth_invariance(dev):
             out = abi_call(d, tuning={key: val})
             for a, b in zip(base, out):
                 assert torch.equal(a, b), (key, val)
+
+
+def test_wide_value_vtile_invariance(dev):
+    """Config 4's V = 256 under every V-tile the plan offers (16, 32 and 64 columns; the default
+    plan takes 32): bit-identical outputs."""
+    inp = _case(64, 2, 300, 2, 128, 256, shift=-2.0)
+    d = dev_inputs(inp, torch.bfloat16, dev)
+    base = abi_call(d)
+    for vt in (16, 32, 64):
+        out = abi_call(d, tuning=dict(v_tile=vt))
+        for a, b in zip(base, out):
+            assert torch.equal(a, b), vt
 
 
 @pytest.mark.parametrize("lens", [None, [100, 61, 239, 64]])
