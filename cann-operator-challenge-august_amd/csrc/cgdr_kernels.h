@@ -183,6 +183,22 @@ __device__ __forceinline__ float f16_nan_to_num(float x) {
 }
 __device__ __forceinline__ float bf16_rnd(float x) { return (float)(__bf16)x; }
 __device__ __forceinline__ float f16_rnd(float x) { return (float)(_Float16)x; }
+
+// Pairs of fp16 values for the contest fast pass (v_cvt_pk_f16_f32, v_pk_add_f16 and
+// v_pk_mul_f16, all round-to-nearest-even).  A sum or product of two fp16 values rounded once
+// to fp16 equals the reference's float32 operation followed by a cast to fp16: a product of two
+// fp16 significands is exact in float32, and a float32 sum rounded again to fp16 is a double
+// rounding with 24 >= 2 * 11 + 2 bits, which never changes the result.
+typedef __attribute__((ext_vector_type(2))) _Float16 h16x2;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+__device__ __forceinline__ h16x2 to_h16x2(float lo, float hi) {
+  return __builtin_convertvector((f32x2){lo, hi}, h16x2);
+}
+__device__ __forceinline__ h16x2 bf16x2_to_h16x2(unsigned w) { return to_h16x2(bf16_lo(w), bf16_hi(w)); }
+__device__ __forceinline__ unsigned h16x2_to_bf16x2(h16x2 x) {
+  const f32x2 f = __builtin_convertvector(x, f32x2);
+  return pack_bf16x2(f[0], f[1]);
+}
 // Running maximum of |x| over the two bf16 of a word, per half (v_pk_max_u16): the bits of
 // |x| order like |x| as unsigned integers, and every NaN lies above +inf (0x7f80).
 __device__ __forceinline__ unsigned pk_absmax_bf16(unsigned acc, unsigned w) {
@@ -656,12 +672,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             hdp[kt][r] = pack_bf16x2(f16_sat(f16_sat(S[kt][2 * r]) * a), f16_sat(f16_sat(S[kt][2 * r + 1]) * a));
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else if constexpr (CONTEST) {
-          // fast pass: plain fp16 roundings (exact while |S| <= 65504 and 0 <= a <= 1)
+          // fast pass: plain fp16 roundings (exact while |S| <= 65504 and 0 <= a <= 1), as
+          // packed fp16 products of fp16(S) and the fp16 decay a
+          const h16x2 a16 = to_h16x2(a, a);
 #pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const float p0 = f16_rnd(S[kt][2 * r]) * a, p1 = f16_rnd(S[kt][2 * r + 1]) * a;
-            hdp[kt][r] = pack_bf16x2(f16_rnd(p0), f16_rnd(p1));
-          }
+          for (int r = 0; r < 2; ++r)
+            hdp[kt][r] = h16x2_to_bf16x2(to_h16x2(S[kt][2 * r], S[kt][2 * r + 1]) * a16);
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[kt] = S[kt] * a;
@@ -699,12 +715,10 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
               pv[j] = pack_bf16x2(x0, x1);
               pd[j] = pack_bf16x2(f16_sat(x0 * gm[tb][hh][r]), f16_sat(x1 * gm[tb][hh][r + 1]));
             } else {
-              const float y0 = f16_rnd(u0) - f16_rnd(-bf16_rnd(v0));
-              const float y1 = f16_rnd(u1) - f16_rnd(-bf16_rnd(v1));
-              const float x0 = f16_rnd(y0), x1 = f16_rnd(y1);
-              const float z0 = x0 * gm[tb][hh][r], z1 = x1 * gm[tb][hh][r + 1];
-              pv[j] = pack_bf16x2(x0, x1);
-              pd[j] = pack_bf16x2(f16_rnd(z0), f16_rnd(z1));
+              // v16 = fp16(u) - fp16(bf16(W S)) = fp16(u) + fp16(bf16(acc)), acc = -W S
+              const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(v0, v1));
+              pv[j] = h16x2_to_bf16x2(x16);
+              pd[j] = h16x2_to_bf16x2(x16 * to_h16x2(gm[tb][hh][r], gm[tb][hh][r + 1]));
             }
           } else {
             pv[j] = pack_bf16x2(v0, v1);
@@ -738,17 +752,25 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         // NaN, which the fast pass leaves in the new state (seen in the next h snapshot, or in
         // the final state below).
 #pragma unroll
-        for (int kt = 0; kt < KT; ++kt)
+        for (int kt = 0; kt < KT; ++kt) {
+          if constexpr (FULL) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const unsigned hw = hdp[kt][r >> 1];
-            const float hd = (r & 1) ? bf16_hi(hw) : bf16_lo(hw);
-            if constexpr (FULL) {
+            for (int r = 0; r < 4; ++r) {
+              const unsigned hw = hdp[kt][r >> 1];
+              const float hd = (r & 1) ? bf16_hi(hw) : bf16_lo(hw);
               S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[kt][r]))));
-            } else {
-              S[kt][r] = bf16_rnd(hd + bf16_rnd(f16_rnd(bf16_rnd(S[kt][r]))));
+            }
+          } else {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const unsigned up = h16x2_to_bf16x2(bf16x2_to_h16x2(pack_bf16x2(S[kt][2 * r], S[kt][2 * r + 1])));
+              const unsigned hw = hdp[kt][r];
+              const unsigned sw = pack_bf16x2(bf16_lo(hw) + bf16_lo(up), bf16_hi(hw) + bf16_hi(up));
+              S[kt][2 * r] = bf16_lo(sw);
+              S[kt][2 * r + 1] = bf16_hi(sw);
             }
           }
+        }
       }
       wait_lgkm0();
       block_barrier();   // B_c
