@@ -125,6 +125,9 @@ def make_workload_inputs(torch, dev, name: str, seed: int = 0):
     return t, dict(B=B, T=T, H=H, Hg=Hg, K=K, V=V, N=N, NT=NT, chunk_size=64)
 
 
+CPU_SAMPLE_SECONDS = 10.0
+
+
 def head_parallel_cpu(run, n_heads: int, group: int, T: int, repeats: int, what: str):
     """Time an oracle over heads [0, n_heads) of T tokens on the host's cores.
 
@@ -132,7 +135,8 @@ def head_parallel_cpu(run, n_heads: int, group: int, T: int, repeats: int, what:
     per-chunk GEMMs are too small for multi-threaded BLAS, which ran slower than one thread.
     The worker count is chosen by a sweep on the first min(T, 4096) tokens (each count timed
     twice, the faster run kept); the chosen count
-    is then timed on all T tokens (median of `repeats` after that warm-up).  `run(lo, hi, t)`
+    is then timed on all T tokens (median of at least `repeats` runs after that warm-up, and of
+    at least CPU_SAMPLE_SECONDS of timed runs).  `run(lo, hi, t)`
     runs the oracle on heads [lo, hi) and the first t tokens; `group` keeps head slices whole
     multiples of the heads that share a key head."""
     from concurrent.futures import ThreadPoolExecutor
@@ -169,10 +173,14 @@ def head_parallel_cpu(run, n_heads: int, group: int, T: int, repeats: int, what:
             single = min(single, time.perf_counter() - t0)
         progress(f"cpu baseline: {best} worker threads fastest on {ts} tokens "
                  f"({', '.join(f'{c}: {s:.2f} s' for c, s in sweep.items())})")
+        # at least `repeats` runs and at least CPU_SAMPLE_SECONDS of timed CPU work (a bounded
+        # sample: at most 200 runs)
         times = []
-        for i in range(repeats):
+        while len(times) < repeats or (sum(times) < CPU_SAMPLE_SECONDS and len(times) < 200):
             times.append(timed(best, T))
-            progress(f"cpu baseline run {i + 1}/{repeats}: {times[-1]:.2f} s")
+            if len(times) <= repeats or len(times) % 10 == 0:
+                progress(f"cpu baseline run {len(times)}: {times[-1]:.2f} s (total {sum(times):.1f} s)")
+        repeats = len(times)
     t = statistics.median(times)
     return dict(t=t, cores=best, host_cores=cores, sample_tokens=ts,
                 single_thread_tokens_per_s=ts / single,

@@ -199,7 +199,9 @@ def chunk_gated_delta_rule_fwd_h(
             raise ValueError(f"initial_state must have shape {list(want)} ({state_layout}), got {list(initial_state.shape)}")
         h0 = initial_state if initial_state.dtype in _DTYPES else initial_state.float()
         h0 = h0.contiguous()
-    align = 16   # 16-byte rows: direct-to-LDS loads (bf16), vector loads (fp32)
+    # 16-byte rows for the direct-to-LDS (bf16) and vector (fp32) loads; with K or V not a
+    # multiple of 16 the library copies k, w and u into padded rows itself
+    align = 16 if K % 16 == 0 and V % 16 == 0 else k.element_size()
     k, w, u = _prep_input(k, "k", align), _prep_input(w, "w", align), _prep_input(u, "u", align)
 
     h = k.new_empty(B, NT, H, K, V)
@@ -252,7 +254,9 @@ def run(k, w, u, g, initial_state, cu_seqlens, chunk_indices, chunk_size=CHUNK_S
     if initial_state is not None:
         h0 = initial_state.reshape(N, H, K, V)
         h0 = (h0 if h0.dtype in _DTYPES else h0.float()).contiguous()
-    align = 16   # 16-byte rows: direct-to-LDS loads (bf16), vector loads (fp32)
+    # 16-byte rows for the direct-to-LDS (bf16) and vector (fp32) loads; with K or V not a
+    # multiple of 16 the library copies k, w and u into padded rows itself
+    align = 16 if K % 16 == 0 and V % 16 == 0 else k.element_size()
     k, w, u = _prep_input(k, "k", align), _prep_input(w, "w", align), _prep_input(u, "u", align)
     S = torch.empty(B, H, NT, K, V, dtype=k.dtype, device=dev)
     v = torch.empty(B, H, T, V, dtype=u.dtype, device=dev)

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 
 #include "cgdr_fwd_h_dispatch.h"
@@ -165,10 +166,9 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   const int64_t K = a->K, V = a->V;
   const int es = a->in_dtype == CGDR_BF16 ? 2 : 4;
   if (K < 32 || K % 16 != 0)
-    return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (must be a multiple of 16 in [32, 256])", (long long)K);
+    return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (must be at least 32)", (long long)K);
   const int kd = kernel_kd(K);
-  if (V % 16 != 0)
-    return fail(CGDR_ERR_UNSUPPORTED, "V=%lld is not supported (must be a multiple of 16)", (long long)V);
+  if (V % 16 != 0) return fail(CGDR_ERR_UNSUPPORTED, "V=%lld is not a multiple of 16", (long long)V);
   const int row_align = 16;   // bf16: direct-to-LDS loads; fp32: 16-byte vector loads
   const void* ptrs[] = {a->k, a->w, a->u};
   const int64_t* strides[] = {a->stride_k, a->stride_w, a->stride_u};
@@ -390,6 +390,135 @@ hipError_t launch_g_relayout(const cgdr_fwd_h_args* a, float* gt, hipStream_t s)
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------
+// K or V not a multiple of 16 (the reference accepts any K = V in [32, 256]): the call runs on
+// dense copies padded to multiples of 16 in the workspace.  k, w, u and the initial state are
+// copied in with zeros in the padding, the kernels run on the padded shapes (exact: zero key
+// columns and value columns contribute nothing, and the padding rows of the state stay zero),
+// and h, v_new and the final state are copied out.  Rows of k/w/u whose length is not a
+// multiple of 8 elements are not 16-byte aligned, which the direct-to-LDS loads need.
+
+bool needs_repack(const cgdr_fwd_h_args* a) { return a != nullptr && (a->K % 16 != 0 || a->V % 16 != 0); }
+
+struct Repack {
+  cgdr_fwd_h_args pa;   // the padded call; its buffer pointers are offsets from the workspace
+  size_t off_k, off_w, off_u, off_h0, off_h, off_v, off_f, bytes;
+};
+
+int64_t round16(int64_t x) { return (x + 15) / 16 * 16; }
+size_t round256(size_t x) { return (x + 255) & ~(size_t)255; }
+int elem_bytes(int32_t dtype) { return dtype == CGDR_BF16 ? 2 : 4; }
+
+// The padded call, with buffers at workspace offsets from `base` (16-byte aligned).
+Repack make_repack(const cgdr_fwd_h_args* a, char* base) {
+  Repack r;
+  r.pa = *a;
+  cgdr_fwd_h_args& p = r.pa;
+  const int64_t B = a->B, T = a->T, H = a->H, Hg = a->Hg, N = a->N, NT = a->NT;
+  const int64_t Kp = round16(a->K), Vp = round16(a->V);
+  const size_t es = elem_bytes(a->in_dtype);
+  size_t off = 0;
+  auto take = [&](size_t bytes) { const size_t o = off; off += round256(bytes); return o; };
+  r.off_k = take((size_t)(B * T * Hg * Kp) * es);
+  r.off_w = take((size_t)(B * T * H * Kp) * es);
+  r.off_u = take((size_t)(B * T * H * Vp) * es);
+  r.off_h0 = a->initial_state ? take((size_t)(N * H * Kp * Vp) * elem_bytes(a->h0_dtype)) : 0;
+  r.off_h = take((size_t)(B * NT * H * Kp * Vp) * es);
+  r.off_v = a->v_new ? take((size_t)(B * T * H * Vp) * es) : 0;
+  r.off_f = a->final_state ? take((size_t)(N * H * Kp * Vp) * elem_bytes(a->final_dtype)) : 0;
+  r.bytes = off;
+  p.K = Kp;
+  p.V = Vp;
+  p.k = base + r.off_k;
+  p.w = base + r.off_w;
+  p.u = base + r.off_u;
+  p.initial_state = a->initial_state ? base + r.off_h0 : nullptr;
+  p.h = base + r.off_h;
+  p.v_new = a->v_new ? base + r.off_v : nullptr;
+  p.final_state = a->final_state ? base + r.off_f : nullptr;
+  const int64_t sk[3] = {T * Hg * Kp, Hg * Kp, Kp}, sw[3] = {T * H * Kp, H * Kp, Kp};
+  const int64_t su[3] = {T * H * Vp, H * Vp, Vp}, sh[3] = {NT * H * Kp * Vp, H * Kp * Vp, Kp * Vp};
+  const int64_t s0[2] = {H * Kp * Vp, Kp * Vp};
+  memcpy(p.stride_k, sk, sizeof sk);
+  memcpy(p.stride_w, sw, sizeof sw);
+  memcpy(p.stride_u, su, sizeof su);
+  memcpy(p.stride_v, su, sizeof su);
+  memcpy(p.stride_h, sh, sizeof sh);
+  memcpy(p.stride_h0, s0, sizeof s0);
+  memcpy(p.stride_final, s0, sizeof s0);
+  return r;
+}
+
+// Copies between a strided tensor of rows (row (i0, i1, i2, r) at i0*s0 + i1*s1 + i2*s2 + r*s3,
+// C contiguous elements) and a dense one of n0 x n1 x n2 x Rp rows of Cp elements.  Into the
+// dense side, rows r >= R and columns c >= C are zero; out of it, only r < R, c < C are written.
+struct RowSet {
+  int64_t n0, n1, n2, R, Rp, C, Cp;
+  int64_t s0, s1, s2, s3;
+};
+
+template <typename E>
+__global__ void __launch_bounds__(256) cgdr_repack_kernel(const E* __restrict__ src, E* __restrict__ dst,
+                                                          RowSet rs, int to_dense) {
+  const int64_t total = rs.n0 * rs.n1 * rs.n2 * rs.Rp * rs.Cp;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    int64_t q = i;
+    const int64_t c = q % rs.Cp;
+    q /= rs.Cp;
+    const int64_t r = q % rs.Rp;
+    q /= rs.Rp;
+    const int64_t i2 = q % rs.n2;
+    q /= rs.n2;
+    const int64_t i1 = q % rs.n1;
+    const int64_t i0 = q / rs.n1;
+    const bool real = r < rs.R && c < rs.C;
+    const int64_t strided = i0 * rs.s0 + i1 * rs.s1 + i2 * rs.s2 + r * rs.s3 + c;
+    if (to_dense) dst[i] = real ? src[strided] : E(0);
+    else if (real) dst[strided] = src[i];
+  }
+}
+
+hipError_t repack(const void* src, void* dst, int esize, const RowSet& rs, bool to_dense, hipStream_t s) {
+  const int64_t total = rs.n0 * rs.n1 * rs.n2 * rs.Rp * rs.Cp;
+  if (total == 0) return hipSuccess;
+  const unsigned grid = (unsigned)std::min<int64_t>((total + 255) / 256, 1 << 16);
+  if (esize == 2)
+    hipLaunchKernelGGL(cgdr_repack_kernel<uint16_t>, dim3(grid), dim3(256), 0, s, (const uint16_t*)src,
+                       (uint16_t*)dst, rs, (int)to_dense);
+  else
+    hipLaunchKernelGGL(cgdr_repack_kernel<uint32_t>, dim3(grid), dim3(256), 0, s, (const uint32_t*)src,
+                       (uint32_t*)dst, rs, (int)to_dense);
+  return hipGetLastError();
+}
+
+// A fake, aligned workspace base for sizing the padded call on the host.
+char* const kSizingBase = (char*)(uintptr_t)(1u << 20);
+
+// The padded call of a repacked one, validated, with its plan.
+cgdr_status plan_repack(const cgdr_fwd_h_args* a, char* base, Repack* r, Plan* pl) {
+  cgdr_status st = validate(a);
+  if (st != CGDR_OK) return st;
+  if (a->K < 32) return fail(CGDR_ERR_UNSUPPORTED, "K=%lld is not supported (must be at least 32)", (long long)a->K);
+  *r = make_repack(a, base);
+  return make_plan(&r->pa, pl);
+}
+
+// Workspace bytes of any call (the padded copies first when repacked).
+cgdr_status workspace_need(const cgdr_fwd_h_args* a, size_t* need) {
+  Plan pl;
+  if (needs_repack(a)) {
+    Repack r;
+    cgdr_status st = plan_repack(a, kSizingBase, &r, &pl);
+    if (st != CGDR_OK) return st;
+    *need = r.bytes + workspace_bytes_of(&r.pa, pl);
+    return CGDR_OK;
+  }
+  cgdr_status st = make_plan(a, &pl);
+  if (st != CGDR_OK) return st;
+  *need = workspace_bytes_of(a, pl);
+  return CGDR_OK;
+}
+
 // Scratch of cgdr_fwd_h_launch_no_alloc: a file-scope device array that every GPU the library
 // runs on holds (its own copy, at its own address) until the process ends.  Host code never
 // passes the array's name to a kernel or a copy: its device address is looked up once per
@@ -447,18 +576,17 @@ const char* cgdr_status_string(cgdr_status status) {
 
 cgdr_status cgdr_fwd_h_workspace_size(const cgdr_fwd_h_args* args, size_t* workspace_bytes) {
   if (workspace_bytes == nullptr) return fail(CGDR_ERR_NULLPTR, "workspace_bytes is NULL");
-  Plan pl;
-  cgdr_status st = make_plan(args, &pl);
-  if (st != CGDR_OK) return st;
-  *workspace_bytes = workspace_bytes_of(args, pl);
-  return CGDR_OK;
+  return workspace_need(args, workspace_bytes);
 }
 
 cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* plan) {
   if (plan == nullptr) return fail(CGDR_ERR_NULLPTR, "plan is NULL");
   Plan pl;
-  cgdr_status st = make_plan(args, &pl);
+  Repack r;
+  const bool rp = needs_repack(args);
+  cgdr_status st = rp ? plan_repack(args, kSizingBase, &r, &pl) : make_plan(args, &pl);
   if (st != CGDR_OK) return st;
+  if (rp) args = &r.pa;   // the plan of the padded call
   plan->kernel = pl.kernel;
   plan->v_tile = 16 * pl.ncw;
   plan->compute_waves = pl.ncw;
@@ -474,6 +602,47 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
 }
 
 cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size_t workspace_bytes, void* stream) {
+  if (needs_repack(args)) {
+    size_t need = 0;
+    cgdr_status st = workspace_need(args, &need);
+    if (st != CGDR_OK) return st;
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(CGDR_ERR_INVALID, "workspace of %zu bytes required (got %zu)", need,
+                  workspace == nullptr ? (size_t)0 : workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(CGDR_ERR_INVALID, "workspace must be 16-byte aligned");
+    Repack r;
+    Plan pl;
+    st = plan_repack(args, (char*)workspace, &r, &pl);
+    if (st != CGDR_OK) return st;
+    const cgdr_fwd_h_args* a = args;
+    const cgdr_fwd_h_args& p = r.pa;
+    const int es = elem_bytes(a->in_dtype);
+    hipStream_t s = (hipStream_t)stream;
+    // state blocks: rows x columns of K x V (rows of V) or V x K (rows of K)
+    const bool vk = a->state_layout == CGDR_STATE_VK;
+    const int64_t sr = vk ? a->V : a->K, srp = vk ? p.V : p.K, sc = vk ? a->K : a->V, scp = vk ? p.K : p.V;
+    const RowSet k_rows{a->B, a->T, a->Hg, 1, 1, a->K, p.K, a->stride_k[0], a->stride_k[1], a->stride_k[2], 0};
+    const RowSet w_rows{a->B, a->T, a->H, 1, 1, a->K, p.K, a->stride_w[0], a->stride_w[1], a->stride_w[2], 0};
+    const RowSet u_rows{a->B, a->T, a->H, 1, 1, a->V, p.V, a->stride_u[0], a->stride_u[1], a->stride_u[2], 0};
+    const RowSet v_rows{a->B, a->T, a->H, 1, 1, a->V, p.V, a->stride_v[0], a->stride_v[1], a->stride_v[2], 0};
+    const RowSet h_rows{a->B, a->NT, a->H, a->K, p.K, a->V, p.V, a->stride_h[0], a->stride_h[1], a->stride_h[2], a->V};
+    const RowSet h0_rows{a->N, a->H, 1, sr, srp, sc, scp, a->stride_h0[0], a->stride_h0[1], 0, sc};
+    const RowSet f_rows{a->N, a->H, 1, sr, srp, sc, scp, a->stride_final[0], a->stride_final[1], 0, sc};
+    hipError_t e = repack(a->k, (void*)p.k, es, k_rows, true, s);
+    if (e == hipSuccess) e = repack(a->w, (void*)p.w, es, w_rows, true, s);
+    if (e == hipSuccess) e = repack(a->u, (void*)p.u, es, u_rows, true, s);
+    if (e == hipSuccess && a->initial_state)
+      e = repack(a->initial_state, (void*)p.initial_state, elem_bytes(a->h0_dtype), h0_rows, true, s);
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "repack launch failed: %s", hipGetErrorString(e));
+    st = cgdr_fwd_h_launch(&p, (char*)workspace + r.bytes, workspace_bytes - r.bytes, stream);
+    if (st != CGDR_OK) return st;
+    e = repack(p.h, a->h, es, h_rows, false, s);
+    if (e == hipSuccess && a->v_new) e = repack(p.v_new, a->v_new, es, v_rows, false, s);
+    if (e == hipSuccess && a->final_state)
+      e = repack(p.final_state, a->final_state, elem_bytes(a->final_dtype), f_rows, false, s);
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "repack launch failed: %s", hipGetErrorString(e));
+    return CGDR_OK;
+  }
   Plan pl;
   cgdr_status st = make_plan(args, &pl);
   if (st != CGDR_OK) return st;
@@ -553,10 +722,9 @@ cgdr_status cgdr_prepare_chunk_indices(const int64_t* cu_seqlens, int64_t n_seq,
 }
 
 cgdr_status cgdr_fwd_h_launch_no_alloc(const cgdr_fwd_h_args* args, void* stream) {
-  Plan pl;
-  cgdr_status st = make_plan(args, &pl);
+  size_t need = 0;
+  cgdr_status st = workspace_need(args, &need);
   if (st != CGDR_OK) return st;
-  const size_t need = workspace_bytes_of(args, pl);
   if (need > kNoAllocScratchBytes)
     return fail(CGDR_ERR_UNSUPPORTED,
                 "this call needs %zu bytes of scratch; cgdr_fwd_h_launch_no_alloc holds %zu (pass g with token "

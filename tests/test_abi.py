@@ -171,9 +171,8 @@ def test_launch_rejects_missing_or_short_workspace(lib):
     (lambda a: setattr(a, "NT", 5), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "N", 2), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "K", 300), _abi.CGDR_ERR_INVALID),         # K > 256
-    (lambda a: setattr(a, "K", 100), _abi.CGDR_ERR_UNSUPPORTED),   # not a multiple of 16
-    (lambda a: setattr(a, "K", 16), _abi.CGDR_ERR_UNSUPPORTED),    # below 32
-    (lambda a: setattr(a, "V", 24), _abi.CGDR_ERR_UNSUPPORTED),
+    (lambda a: setattr(a, "K", 16), _abi.CGDR_ERR_UNSUPPORTED),    # below 32, as the reference
+    (lambda a: setattr(a, "K", 20), _abi.CGDR_ERR_UNSUPPORTED),
     (lambda a: setattr(a, "in_dtype", 7), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "state_layout", 2), _abi.CGDR_ERR_INVALID),
     (lambda a: setattr(a, "reserved", 1), _abi.CGDR_ERR_INVALID),
@@ -294,6 +293,31 @@ def test_plan_wide_tiles_without_helpers(lib, B, T, H, K):
     tiles with one load wave and no helpers on MI355X."""
     p = _abi.get_plan(_mi355x(_args(B=B, T=T, H=H, Hg=H, K=K, V=K)))
     assert (p.v_tile, p.helpers, p.load_waves) == (32, 0, 1)
+
+
+@pytest.mark.parametrize("K,V,dtype", [(100, 100, _abi.CGDR_BF16), (33, 33, _abi.CGDR_BF16),
+                                       (128, 100, _abi.CGDR_F32), (200, 200, _abi.CGDR_BF16)])
+def test_workspace_holds_padded_copies(lib, K, V, dtype):
+    """K or V not a multiple of 16 (the reference accepts any K = V in [32, 256]): the call runs
+    on copies padded to multiples of 16, which the workspace holds (k, w, u, h0, h, v_new and
+    the final state, each rounded up to 256 bytes) ahead of the padded call's own workspace."""
+    B, T, H, Hg = 1, 256, 4, 2
+    a = _mi355x(_args(B=B, T=T, H=H, Hg=Hg, K=K, V=V, dtype=dtype))
+    a.initial_state = a.final_state = a.v_new = 1 << 24
+    a.h0_dtype = a.final_dtype = _abi.CGDR_F32
+    a.stride_h0[:] = [H * K * V, K * V]
+    a.stride_final[:] = [H * K * V, K * V]
+    a.stride_v[:] = [T * H * V, H * V, V]
+    st, n = _status(a)
+    assert st == _abi.CGDR_OK, _abi.last_error()
+    Kp, Vp, NT = (K + 15) // 16 * 16, (V + 15) // 16 * 16, T // 64
+    es = 2 if dtype == _abi.CGDR_BF16 else 4
+    r256 = lambda x: (x + 255) // 256 * 256
+    copies = (r256(B * T * Hg * Kp * es) + r256(B * T * H * Kp * es) + r256(B * T * H * Vp * es)
+              + r256(H * Kp * Vp * 4) + r256(B * NT * H * Kp * Vp * es) + r256(B * T * H * Vp * es)
+              + r256(H * Kp * Vp * 4))
+    assert n == copies      # the padded call itself needs no workspace here (no g, no helpers)
+    assert _abi.get_plan(a).v_tile >= 16
 
 
 def test_tuning_overrides_and_rejections(lib):

@@ -281,7 +281,7 @@ def test_contest_kernel_saturation(dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("D", [48, 96, 160, 192])
+@pytest.mark.parametrize("D", [48, 96, 160, 192, 33, 100])
 def test_contest_kernel_padded_head_dims(dev, D):
     """Contest numerics at key dims between the kernels' instantiated 32/64/128/256 (zero-padded
     tiles and state rows on chip): against the O2 oracle, with the generator's distributions

@@ -147,14 +147,14 @@ def test_config4_full_size(dev):
 # rows are zero-padded on chip (the reference accepts any K = V in [32, 256])
 @pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (64, 128), (128, 64), (256, 256), (256, 64),
                                  (48, 48), (80, 80), (96, 96), (112, 112), (160, 160), (192, 192), (224, 224),
-                                 (96, 128)])
+                                 (96, 128), (33, 33), (100, 100), (200, 200), (128, 100), (72, 40)])
 def test_head_dims_bf16(dev, K, V):
     inp = _case(10 + K + V, 1, 200, 2, K, V, shift=4.0, profile="wy")
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
 @pytest.mark.parametrize("K,V", [(32, 32), (64, 64), (128, 128), (128, 64), (48, 48), (96, 96), (192, 192),
-                                 (256, 256)])
+                                 (256, 256), (100, 100), (37, 50)])
 def test_head_dims_fp32(dev, K, V):
     inp = _case(20 + K + V, 2, 130, 2, K, V, dtype="f32", gate="linear")
     out = abi_call(dev_inputs(inp, torch.float32, dev))
@@ -251,7 +251,7 @@ def test_optional_outputs_and_dtypes(dev):
     assert torch.equal(h, h2)
 
 
-@pytest.mark.parametrize("dtype,K,V", [("bf16", 128, 128), ("bf16", 96, 64), ("f32", 64, 32)])
+@pytest.mark.parametrize("dtype,K,V", [("bf16", 128, 128), ("bf16", 96, 64), ("f32", 64, 32), ("bf16", 100, 72)])
 def test_transposed_state_layout(dev, dtype, K, V):
     """state_layout="vk": initial_state and final_state as [N,H,V,K] blocks (the full operator's
     [B,Nv,Dv,Dk] state) give, bit for bit, the transposes of the [N,H,K,V] run, with packed
