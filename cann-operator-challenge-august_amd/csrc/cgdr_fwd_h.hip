@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "cgdr_fwd_h_dispatch.h"
@@ -257,8 +258,9 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
   // Helper workgroups (one per task, on the task's XCD) when the doubled grid still fits the
   // device at one workgroup per CU, so that tasks and helpers are all resident together.
   pl->helpers = 0;
+  // (a progress value holds up to 2^24 - 1 chunks)
   if (pl->kernel != 1 && pl->tasks % xcds == 0 && 2 * pl->tasks <= cus && helpers_req != 0 &&
-      (use_helpers || helpers_req == 1))
+      (use_helpers || helpers_req == 1) && a->NT < (1 << 24))
     pl->helpers = 1;
   return CGDR_OK;
 }
@@ -665,14 +667,20 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     p.sg_t = 1;
     p.sg_h = args->T;
   }
-  const size_t nzero = progress_ints(pl) + redo_ints(args, pl);
-  if (nzero > 0) {
-    int32_t* counters = (int32_t*)((char*)workspace + g_bytes);
-    if (pl.helpers) p.progress = counters;
-    if (pl.kernel == 2) p.redo = counters + progress_ints(pl);
-    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, counters, (int64_t)nzero);
+  int32_t* counters = (int32_t*)((char*)workspace + g_bytes);
+  if (pl.helpers) {
+    // The helpers' progress counters are tagged with this launch's epoch instead of being
+    // cleared (one launch fewer per call): a value from another launch reads as no progress.
+    static std::atomic<uint32_t> launches{0};
+    p.progress = counters;
+    p.epoch = 1 + (int32_t)(launches.fetch_add(1, std::memory_order_relaxed) % 255u);
+  }
+  const size_t nredo = redo_ints(args, pl);
+  if (nredo > 0) {
+    p.redo = counters + progress_ints(pl);
+    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, p.redo, (int64_t)nredo);
     e = hipGetLastError();
-    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "counter reset launch failed: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "flag reset launch failed: %s", hipGetErrorString(e));
   }
   switch (kernel_kd(args->K)) {
     case 32: e = cgdr_fwd::launch_kd<32>(p, pl, s); break;

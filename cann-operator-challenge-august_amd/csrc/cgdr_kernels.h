@@ -107,6 +107,7 @@ struct FwdHParams {
   int32_t K;            // key dim, a multiple of 16 up to the kernel's KD: columns K..KD-1 of
                         // the K and W tiles and rows K..KD-1 of the state are zero padding
   int32_t state_vk;     // initial and final state blocks are V x K (rows of K), else K x V
+  int32_t epoch;        // helpers: this launch's tag (1..255) in the top byte of a progress value
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
                         // task (kProgressStride ints; zeroed before launch)
   int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
@@ -527,11 +528,16 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     };
     constexpr int D = STAGES - 1;
     const int* prog_addr = p.progress + task_id * kProgressStride;
+    // A progress value is (epoch << 24) | chunks done; a value left by an earlier launch (other
+    // tag) or never written reads as 0.  The counters are not cleared before a launch.
+    auto progress_of = [&](int v) -> int {
+      return ((unsigned)v >> 24) == (unsigned)p.epoch ? (v & 0xffffff) : 0;
+    };
     int issued = 1 + wave;   // chunk 0 is loaded before the task's first barrier
     int idle = 0;
     const int max_idle = 8 * NC + 4096;
     while (issued < NC) {
-      const int done = poll_l2(prog_addr);
+      const int done = progress_of(poll_l2(prog_addr));
       // Chunks below done + D are already in the task's own loads (a helper that starts late,
       // e.g. on a device shared with other work, skips them instead of touching them again).
       const int lo = done + D;
@@ -1042,7 +1048,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       wait_lgkm0();
       block_barrier();   // B_c
       if (p.helpers && sw == 0 && lane == 0)
-        __hip_atomic_store(p.progress + task_id * kProgressStride, c + 1, __ATOMIC_RELAXED,
+        __hip_atomic_store(p.progress + task_id * kProgressStride,
+                           (int)(((unsigned)p.epoch << 24) | (unsigned)(c + 1)), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
     if (NC > 0) store_chunk(NC - 1);
@@ -1103,7 +1110,7 @@ cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, in
   }
 }
 
-// Zero n int32 counters (the helpers' progress counters) ahead of the chunk kernel; a kernel
+// Zero n int32 flags (the contest pass's per-head flags) ahead of the chunk kernel; a kernel
 // rather than a memset so that the whole call can be captured in a HIP graph.
 static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __restrict__ x, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0;
