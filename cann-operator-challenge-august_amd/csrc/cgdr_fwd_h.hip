@@ -667,21 +667,16 @@ cgdr_status cgdr_fwd_h_launch(const cgdr_fwd_h_args* args, void* workspace, size
     p.sg_t = 1;
     p.sg_h = args->T;
   }
+  // The helpers' progress counters and the contest flags hold this launch's epoch instead of
+  // being cleared before it (no reset launch): a value left by another launch reads as no
+  // progress, or as an unflagged head.
   int32_t* counters = (int32_t*)((char*)workspace + g_bytes);
-  if (pl.helpers) {
-    // The helpers' progress counters are tagged with this launch's epoch instead of being
-    // cleared (one launch fewer per call): a value from another launch reads as no progress.
+  if (pl.helpers || pl.kernel == 2) {
     static std::atomic<uint32_t> launches{0};
-    p.progress = counters;
     p.epoch = 1 + (int32_t)(launches.fetch_add(1, std::memory_order_relaxed) % 255u);
   }
-  const size_t nredo = redo_ints(args, pl);
-  if (nredo > 0) {
-    p.redo = counters + progress_ints(pl);
-    hipLaunchKernelGGL(cgdr::cgdr_zero_i32_kernel, dim3(1), dim3(256), 0, s, p.redo, (int64_t)nredo);
-    e = hipGetLastError();
-    if (e != hipSuccess) return fail(CGDR_ERR_LAUNCH, "flag reset launch failed: %s", hipGetErrorString(e));
-  }
+  if (pl.helpers) p.progress = counters;
+  if (pl.kernel == 2) p.redo = counters + progress_ints(pl);
   switch (kernel_kd(args->K)) {
     case 32: e = cgdr_fwd::launch_kd<32>(p, pl, s); break;
     case 64: e = cgdr_fwd::launch_kd<64>(p, pl, s); break;

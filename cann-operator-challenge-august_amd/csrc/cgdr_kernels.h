@@ -107,10 +107,12 @@ struct FwdHParams {
   int32_t K;            // key dim, a multiple of 16 up to the kernel's KD: columns K..KD-1 of
                         // the K and W tiles and rows K..KD-1 of the state are zero padding
   int32_t state_vk;     // initial and final state blocks are V x K (rows of K), else K x V
-  int32_t epoch;        // helpers: this launch's tag (1..255) in the top byte of a progress value
+  int32_t epoch;        // this launch's tag (1..255): the top byte of a helper's progress value,
+                        // and the value of a contest flag this launch raised
   int32_t* progress;    // helpers: chunk iterations completed per task, one 128-byte line per
-                        // task (kProgressStride ints; zeroed before launch)
-  int32_t* redo;        // contest: one flag per (sequence, head), zeroed before the fast pass
+                        // task (kProgressStride ints; epoch-tagged, not cleared)
+  int32_t* redo;        // contest: one flag per (sequence, head); a head is flagged when its flag
+                        // holds this launch's epoch (flags are not cleared between launches)
 };
 
 constexpr int kProgressStride = 32;
@@ -410,7 +412,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   if (task_id >= p.n_tasks) return;   // uniform per workgroup
   const Task tk = decode_task(p, order_task(p, task_id));
   if constexpr (FULL)
-    if (p.redo[(int64_t)tk.n * p.H + tk.head] == 0) return;   // uniform: the fast pass was exact
+    if (p.redo[(int64_t)tk.n * p.H + tk.head] != p.epoch) return;   // uniform: the fast pass was exact
   const int NC = tk.nc;
   const int vbase = tk.vtile * VT;
   const int hk = tk.head / p.head_ratio;
@@ -796,7 +798,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) bad |= S[kt][r] != S[kt][r];
-      if (__any(bad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
+      if (__any(bad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
     }
     if (p.final_state != nullptr) {
       const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
@@ -1056,7 +1058,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
     if constexpr (NUM == 1)
       if (__any((amax & 0xffffu) > 0x477fu || (amax >> 16) > 0x477fu) && lane == 0)
-        p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
+        p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
   } else if (wave == NCW + L::NSW + NLW) {
     // ------------------------------------------------------------------ gate wave
     // Loads the raw g rows itself, with ordinary loads into registers two chunks ahead, and
@@ -1084,7 +1086,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       block_barrier();   // B_c
     }
     if constexpr (NUM == 1)
-      if (__any(gbad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = 1;
+      if (__any(gbad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
   }
 }
 
@@ -1108,12 +1110,6 @@ cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, in
     const int hh = i >> 6, tt = i & 63;
     if (t0 + tt < T && h0 + hh < H) gt[(b * H + h0 + hh) * T + t0 + tt] = tile[tt][hh];
   }
-}
-
-// Zero n int32 flags (the contest pass's per-head flags) ahead of the chunk kernel; a kernel
-// rather than a memset so that the whole call can be captured in a HIP graph.
-static __global__ void __launch_bounds__(256) cgdr_zero_i32_kernel(int32_t* __restrict__ x, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0;
 }
 
 // =============================================================================================
