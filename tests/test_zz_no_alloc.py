@@ -1,9 +1,10 @@
 """cgdr_fwd_h_launch_no_alloc (the entry point that allocates nothing: its workspace is a static
 per-GPU device array) against cgdr_fwd_h_launch with a caller-allocated workspace, bit for bit.
 
-Two calls in a row, the second smaller, so the second starts from what the first left in the
-shared scratch: token-major g (the head-major relayout of g lives in the scratch), helper
-workgroups (their progress counters), and contest numerics (the per-head redo flags).  The
+Three calls in a row, each smaller than the one before, so each starts from what the last left
+in the shared scratch: token-major g (the head-major relayout of g lives in the scratch), helper
+workgroups (their progress counters), contest numerics (the per-head flags), and a head dim
+that is not a multiple of 16 (the padded copies).  The
 oversize rejection is checked on the host, before anything touches a GPU."""
 
 import ctypes
@@ -36,8 +37,10 @@ def _same(a, b):
 def test_no_alloc_matches_workspace_launch(dev):
     # call 1: 8 heads x 4 V-tiles of 32 columns with helpers (progress counters), token-major g
     # (its relayout: 256 KiB of the scratch); call 2: a smaller packed batch in contest numerics
+    # call 3: K = V = 100, which runs on padded copies held in the scratch too
     cases = [(_inp(1, 8192, 8), dict(helpers=1, v_tile=32), 0),
-             (_inp(2, 1000, 4, cu=np.array([0, 300, 301, 1000], np.int64)), None, 1)]
+             (_inp(2, 1000, 4, cu=np.array([0, 300, 301, 1000], np.int64)), None, 1),
+             (_inp(3, 300, 2, K=100, V=100), None, 0)]
     for inp, tuning, numerics in cases:
         d = dev_inputs(inp, torch.bfloat16, dev)
         assert d["g"].stride(1) != 1   # token-major g: the workspace holds its relayout
