@@ -216,32 +216,43 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
 
   // ---- phase 2b: off-diagonal blocks by column block: wave j computes T_ij for i = j+1 .. 3 in
   // order, T_ij = -T_ii sum_{k=j}^{i-1} A_ik T_kj.  Every A block and diagonal T block is in LDS
-  // after the barrier above, and the T_kj (k > j) it needs are its own earlier results, so no
-  // further barrier is needed.
-  // acc += A[xr.., xc..] T[yr.., yc..] (16x16 blocks; A below the diagonal, T diagonal or below)
-  auto mm = [&](f32x4 acc, int xr, int xc, int yr, int yc) {
+  // after the barrier above, and the T_kj (k > j) it needs are its own earlier results, kept in
+  // registers (their C layout is the B operand layout), so no further barrier is needed and no
+  // LDS write stands between two steps: the blocks are written to LDS once all are done.
+  // acc += A[xr.., xc..] B, with B a 16x16 block of T in C layout
+  auto mm = [&](f32x4 acc, int xr, int xc, const f32x4& B) {
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-      acc = mfma_f32(M[(xr + n) * MS + xc + 4 * G + kk], tval(yr + 4 * G + kk, yc + n), acc);
+    for (int kk = 0; kk < 4; ++kk) acc = mfma_f32(M[(xr + n) * MS + xc + 4 * G + kk], B[kk], acc);
     return acc;
   };
-  // T[tr.., tc..] = -(T_{tr,tr} Y), Y held in C layout
-  auto finish = [&](const f32x4& Y, int tr, int tc) {
+  // -(T_{tr,tr} Y), Y held in C layout
+  auto finish = [&](const f32x4& Y, int tr) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) acc = mfma_f32(tval(tr + n, tr + 4 * G + kk), Y[kk], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) M[(tc + n) * MS + tr + 4 * G + r] = -acc[r];
+    return -acc;
   };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  const int cw = 16 * wave;
+  f32x4 tb[4];   // T_{kb, wave}: the diagonal block from LDS, then this wave's results
+  const f32x4 diag = {tval(cw + 4 * G, cw + n), tval(cw + 4 * G + 1, cw + n), tval(cw + 4 * G + 2, cw + n),
+                      tval(cw + 4 * G + 3, cw + n)};
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) tb[kb] = kb == wave ? diag : z4;
 #pragma unroll
   for (int ib = 1; ib < 4; ++ib) {
     if (ib <= wave) continue;
     f32x4 y = z4;
 #pragma unroll
     for (int kb = 0; kb < 3; ++kb)
-      if (kb >= wave && kb < ib) y = mm(y, 16 * ib, 16 * kb, 16 * kb, 16 * wave);
-    finish(y, 16 * ib, 16 * wave);
+      if (kb >= wave && kb < ib) y = mm(y, 16 * ib, 16 * kb, tb[kb]);
+    tb[ib] = finish(y, 16 * ib);
+  }
+#pragma unroll
+  for (int ib = 1; ib < 4; ++ib) {
+    if (ib <= wave) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[(cw + n) * MS + 16 * ib + 4 * G + r] = tb[ib][r];
   }
   wait_lgkm0();
   wait_vm<0>();   // the prefetch loads (issued two phases ago) have landed
