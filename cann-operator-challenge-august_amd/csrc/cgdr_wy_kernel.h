@@ -12,7 +12,7 @@
 // reference, and its device stage 1, op_kernel/arch22/chunk_gated_delta_rule_stage1.h.)
 //
 // Phases, separated by workgroup barriers:
-//   0  DMA of the k tile into LDS; wave 0 forms g (each lane sums a_0..a_i in order, which is
+//   0  DMA of the k tile into LDS by waves 0-2; wave 3 forms g (each lane sums a_0..a_i in order, which is
 //      the sequential cumsum bit for bit), beta e^g and beta.  Then each wave touches its share
 //      of this unit's v rows into L2.
 //   1  S = k k^T with bf16 MFMA (wave w: columns i = 16w..16w+15, operands read from the k tile),
@@ -101,22 +101,34 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
   __bf16* wb = (__bf16*)p.w + b * p.sw_b + start * p.sw_t + head * p.sw_h;
   __bf16* ub = (__bf16*)p.u + b * p.su_b + start * p.su_t + head * p.su_h;
 
-  // ---- phase 0: k tile (rows past the chunk end zero-filled); the v tile follows in phase 3
+  // ---- phase 0: k tile (rows past the chunk end zero-filled), by waves 0-2; the v tile
+  // follows in phase 3.  Wave 3 meanwhile loads beta and the log-decays and forms g, so that
+  // its waits on those loads do not also wait for DMAs of its own (vmcnt counts both).  A full
+  // chunk issues its DMAs in one uniform branch, without a per-lane condition around each.
   const uint32_t lds0 = (uint32_t)(uintptr_t)((lds_char*)smem);
   {
     const int64_t krow = p.sk_t * 2;
+    if (len == 64) {
 #pragma unroll
-    for (int m = 0; m < L::DMA_K; ++m) {
-      if (m % 4 != wave) continue;
-      const int r = m * L::RPDK + lane / L::PK, c = lane % L::PK;
-      if (r < len)
+      for (int m = 0; m < L::DMA_K; ++m) {
+        if (m % 3 != wave) continue;
+        const int r = m * L::RPDK + lane / L::PK, c = lane % L::PK;
         dma_b128(kb, (uint32_t)(r * krow) + 16u * (uint32_t)(c ^ swz_k<L::PK>(r)), lds0 + L::K_OFF + 1024u * m);
-      else
-        *(u32x4*)(smem + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < L::DMA_K; ++m) {
+        if (m % 3 != wave) continue;
+        const int r = m * L::RPDK + lane / L::PK, c = lane % L::PK;
+        if (r < len)
+          dma_b128(kb, (uint32_t)(r * krow) + 16u * (uint32_t)(c ^ swz_k<L::PK>(r)), lds0 + L::K_OFF + 1024u * m);
+        else
+          *(u32x4*)(smem + L::K_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+      }
     }
   }
   float* GA = (float*)(smem + L::G_OFF);
-  if (wave == 0) {
+  if (wave == 3) {
     float bt = 0.f, at = 0.f;
     if (lane < len) {
       const int64_t ob = b * p.sb_b + (start + lane) * p.sb_t + head * p.sb_h;
