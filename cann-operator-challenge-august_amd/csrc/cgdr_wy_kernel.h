@@ -316,14 +316,23 @@ __global__ void __launch_bounds__(256) cgdr_wy_bf16_kernel(const WyParams p) {
 
   {
     const int64_t vrow = p.sv_t * 2;
+    if (len == 64) {   // a full chunk: one uniform branch, no per-lane condition per DMA
 #pragma unroll
-    for (int m = 0; m < L::DMA_V; ++m) {
-      if ((L::DMA_K + m) % 4 != wave) continue;
-      const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
-      if (r < len)
+      for (int m = 0; m < L::DMA_V; ++m) {
+        if ((L::DMA_K + m) % 4 != wave) continue;
+        const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
         dma_b128(vb, (uint32_t)(r * vrow) + 16u * (uint32_t)(c ^ swz_k<L::PV>(r)), lds0 + L::V_OFF + 1024u * m);
-      else
-        *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < L::DMA_V; ++m) {
+        if ((L::DMA_K + m) % 4 != wave) continue;
+        const int r = m * L::RPDV + lane / L::PV, c = lane % L::PV;
+        if (r < len)
+          dma_b128(vb, (uint32_t)(r * vrow) + 16u * (uint32_t)(c ^ swz_k<L::PV>(r)), lds0 + L::V_OFF + 1024u * m);
+        else
+          *(u32x4*)(smem + L::V_OFF + 1024 * m + 16 * lane) = u32x4{0, 0, 0, 0};
+      }
     }
   }
   // One unit: columns 32 pp + 8 G .. +7 of the lane's token, bf16-packed
