@@ -352,3 +352,21 @@ def test_wrapper_refuses_cpu_tensors():
     w = torch.zeros(1, 64, 1, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="HIP device"):
         cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, w)
+
+
+def test_plan_accepts_random_configurations(lib):
+    """Every configuration of the random GPU parity cases (tests/test_gpu_random.py) is planned:
+    its head dims, batch layout, dtype, numerics and tuning fields are all accepted, as for
+    MI355X."""
+    import test_gpu_random as R
+    for i in range(R.CASES):
+        c = R.draw(i)
+        dt = _abi.CGDR_F32 if c["dtype"] == "f32" else _abi.CGDR_BF16
+        a = _args(B=c["B"], T=c["T"], H=c["H"], Hg=c["Hg"], K=c["K"], V=c["V"], dtype=dt,
+                  varlen=None if c["cu"] is None else c["cu"].tolist())
+        a.g = 1 << 24
+        a.stride_g[:] = [c["T"] * c["H"], c["H"], 1]
+        a.numerics = 1 if c["contest"] else 0
+        _mi355x(a, **c["tuning"])
+        p = _abi.get_plan(a)
+        assert p.workgroups > 0, (i, c)
