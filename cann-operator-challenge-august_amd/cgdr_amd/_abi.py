@@ -12,7 +12,7 @@ import ctypes
 import os
 
 CHUNK_SIZE = 64
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CGDR_OK = 0
 CGDR_ERR_NULLPTR = 1
@@ -64,7 +64,7 @@ class FwdHTuning(ctypes.Structure):
         ("helper_waves", ctypes.c_int32),
         ("cu_count", ctypes.c_int32),
         ("xcd_count", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("row_split", ctypes.c_int32),
     ]
 
 
@@ -134,6 +134,7 @@ class FwdHPlan(ctypes.Structure):
         ("load_waves", ctypes.c_int32),
         ("cu_count", ctypes.c_int32),
         ("xcd_count", ctypes.c_int32),
+        ("row_split", ctypes.c_int32),
     ]
 
 

@@ -112,7 +112,7 @@ cgdr_status validate(const cgdr_fwd_h_args* a) {
   return CGDR_OK;
 }
 
-int bf16_max_stages(int64_t K, int ncw, int nlw);
+int bf16_max_stages(int64_t K, int ncw, int nlw, int rs);
 
 bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
 
@@ -145,7 +145,7 @@ cgdr_status check_tuning(const cgdr_fwd_h_tuning* tu) {
   if (tu->helper_lead < -1) return fail(CGDR_ERR_INVALID, "tuning.helper_lead must be >= -1");
   if (tu->helper_waves < 0 || tu->helper_waves > 16) return fail(CGDR_ERR_INVALID, "tuning.helper_waves must be in [0, 16]");
   if (tu->cu_count < 0 || tu->xcd_count < 0) return fail(CGDR_ERR_INVALID, "tuning.cu_count/xcd_count must be >= 0");
-  if (tu->reserved != 0) return fail(CGDR_ERR_INVALID, "tuning.reserved must be 0");
+  if (tu->row_split < 0 || tu->row_split > 2) return fail(CGDR_ERR_INVALID, "tuning.row_split must be 0, 1 or 2");
   return CGDR_OK;
 }
 
@@ -223,6 +223,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (a->in_dtype == CGDR_BF16 && V % 32 == 0 && pairs * (V / 16) > cus) ncw = 2;
   }
   if (V % (16 * ncw) != 0) ncw = 1;
+  pl->rs = 1;
   if (a->in_dtype == CGDR_F32) {
     pl->kernel = 1;
     pl->ncw = ncw;
@@ -244,14 +245,23 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     if (nlw == 0) nlw = (use_helpers || kd == 256 || ncw == 2) ? 1 : 2;
     if (pl->kernel == 2 && nlw == 4) nlw = 2;   // contest instantiations: 1 or 2 load waves
     if (kd == 256) nlw = 1;
-    while (nlw > 1 && 2 * ncw + nlw + 1 > 8) nlw /= 2;
+    // Row split (two compute waves per 16 columns, each with half of the state rows): for the
+    // contest numerics, whose per-element casts make the compute waves the bound.  It needs
+    // an even number of 32-row state blocks (K of 64 or 128 here) and at most 8 waves.
+    int rs = tu != nullptr ? tu->row_split : 0;
+    if (rs == 0) rs = pl->kernel == 2 ? 2 : 1;
+    if (rs == 2 && !(kd == 64 || kd == 128) ) rs = 1;
+    if (rs == 2 && ncw > 2) rs = 1;
+    while (nlw > 1 && (rs + 1) * ncw + nlw + 1 > 8) nlw /= 2;
+    if (rs == 2 && bf16_max_stages(K, ncw, nlw, 2) == 0) rs = 1;
+    pl->rs = rs;
     pl->nlw = nlw;
     int stages = tu != nullptr ? tu->stages : 0;
     // deepest ring that fits the LDS and the vmcnt range
-    const int max_stages = bf16_max_stages(K, ncw, nlw);
+    const int max_stages = bf16_max_stages(K, ncw, nlw, rs);
     if (stages < 2 || stages > max_stages) stages = max_stages;
     pl->stages = stages;
-    pl->threads = 64 * (ncw + nlw + ncw + 1);   // compute, load, store (one per compute), gate
+    pl->threads = 64 * (rs * ncw + nlw + ncw + 1);   // compute, load, store (one per 16 columns), gate
   }
   pl->tasks = a->N * a->H * (V / (16 * ncw));
   if (pl->tasks > kMaxTasks) return fail(CGDR_ERR_UNSUPPORTED, "too many tasks (%lld)", (long long)pl->tasks);
@@ -307,28 +317,38 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
 // Compile-time layout facts of the bf16 kernel instantiation a plan selects.
 template <int KD, typename F>
 auto with_bf16_config(const Plan& pl, F f) {
-  auto by_nlw = [&](auto ncw) {
-    constexpr int NCW = decltype(ncw)::value;
-    auto by_stages = [&](auto nlw) {
-      constexpr int NLW = decltype(nlw)::value;
-      if (pl.stages == 4) return f(cgdr::Bf16Layout<KD, NCW, NLW, 4>{});
-      if (pl.stages == 3) return f(cgdr::Bf16Layout<KD, NCW, NLW, 3>{});
-      return f(cgdr::Bf16Layout<KD, NCW, NLW, 2>{});
+  auto by_rs = [&](auto rs) {
+    constexpr int RS = decltype(rs)::value;
+    auto by_nlw = [&](auto ncw) {
+      constexpr int NCW = decltype(ncw)::value;
+      auto by_stages = [&](auto nlw) {
+        constexpr int NLW = decltype(nlw)::value;
+        if (pl.stages == 4) return f(cgdr::Bf16Layout<KD, NCW, NLW, 4, RS>{});
+        if (pl.stages == 3) return f(cgdr::Bf16Layout<KD, NCW, NLW, 3, RS>{});
+        return f(cgdr::Bf16Layout<KD, NCW, NLW, 2, RS>{});
+      };
+      if (pl.nlw == 1) return by_stages(std::integral_constant<int, 1>{});
+      if (pl.nlw == 4) return by_stages(std::integral_constant<int, 4>{});
+      return by_stages(std::integral_constant<int, 2>{});
     };
-    if (pl.nlw == 1) return by_stages(std::integral_constant<int, 1>{});
-    if (pl.nlw == 4) return by_stages(std::integral_constant<int, 4>{});
-    return by_stages(std::integral_constant<int, 2>{});
+    if (pl.ncw == 4) return by_nlw(std::integral_constant<int, 4>{});
+    if (pl.ncw == 2) return by_nlw(std::integral_constant<int, 2>{});
+    return by_nlw(std::integral_constant<int, 1>{});
   };
-  if (pl.ncw == 4) return by_nlw(std::integral_constant<int, 4>{});
-  if (pl.ncw == 2) return by_nlw(std::integral_constant<int, 2>{});
-  return by_nlw(std::integral_constant<int, 1>{});
+  if (pl.rs == 2) return by_rs(std::integral_constant<int, 2>{});
+  return by_rs(std::integral_constant<int, 1>{});
 }
 
-int bf16_max_stages(int64_t K, int ncw, int nlw) {
+int bf16_max_stages(int64_t K, int ncw, int nlw, int rs) {
   auto pick = [&](auto kd) -> int {
     constexpr int KD = decltype(kd)::value;
     auto by_ncw = [&](auto c) -> int {
       constexpr int NCW = decltype(c)::value;
+      if (rs == 2) {
+        if (nlw == 1) return cgdr::bf16_max_stages<KD, NCW, 1, 2>();
+        if (nlw == 4) return cgdr::bf16_max_stages<KD, NCW, 4, 2>();
+        return cgdr::bf16_max_stages<KD, NCW, 2, 2>();
+      }
       if (nlw == 1) return cgdr::bf16_max_stages<KD, NCW, 1>();
       if (nlw == 4) return cgdr::bf16_max_stages<KD, NCW, 4>();
       return cgdr::bf16_max_stages<KD, NCW, 2>();
@@ -591,7 +611,7 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
   if (rp) args = &r.pa;   // the plan of the padded call
   plan->kernel = pl.kernel;
   plan->v_tile = 16 * pl.ncw;
-  plan->compute_waves = pl.ncw;
+  plan->compute_waves = pl.ncw * pl.rs;
   plan->total_waves = pl.threads / 64;
   plan->stages = pl.stages;
   plan->lds_bytes = lds_bytes_of(pl, args->K);
@@ -600,6 +620,7 @@ cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* pl
   plan->load_waves = pl.nlw;
   plan->cu_count = pl.cus;
   plan->xcd_count = pl.xcds;
+  plan->row_split = pl.rs;
   return CGDR_OK;
 }
 

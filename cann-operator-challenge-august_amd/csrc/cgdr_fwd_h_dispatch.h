@@ -16,7 +16,8 @@ namespace cgdr_fwd {
 struct Plan {
   int kernel;        // 0 bf16 pipeline, 1 fp32, 2 bf16 with the contest numerics (two passes)
   int helpers;       // bf16: one L2-prefetch workgroup per task
-  int ncw;           // compute waves (Vt = 16 * ncw)
+  int ncw;           // 16-column blocks (Vt = 16 * ncw)
+  int rs;            // bf16 pipeline: compute waves per 16-column block (2: state rows split)
   int nlw;           // load waves (bf16 pipeline)
   int stages;        // LDS ring depth (bf16 pipeline)
   int threads;
@@ -25,11 +26,11 @@ struct Plan {
   int xcds;
 };
 
-template <int KD, int NCW, int NLW, int STAGES, int NUM>
+template <int KD, int NCW, int NLW, int STAGES, int NUM, int RS>
 hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
-  using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES>;
+  using L = cgdr::Bf16Layout<KD, NCW, NLW, STAGES, RS>;
   const unsigned grid = (unsigned)(p.helpers ? 2 * tasks : tasks);
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, NUM>), dim3(grid),
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_bf16_kernel<KD, NCW, NLW, STAGES, NUM, RS>), dim3(grid),
                      dim3(L::THREADS), 0, stream, p);
   return hipGetLastError();
 }
@@ -41,32 +42,42 @@ hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stre
   return hipGetLastError();
 }
 
-// NUM: the kernel's numerics mode (0 default, 1 contest fast pass, 2 contest full pass)
-template <int KD, int NCW, int NLW, int NUM>
+// NUM: the kernel's numerics mode (0 default, 1 contest fast pass, 2 contest full pass).
+// Configurations that do not fit (LDS, vmcnt range, waves) are not instantiated; the plan never
+// selects them.
+template <int KD, int NCW, int NLW, int NUM, int RS>
 hipError_t dispatch_bf16_stages(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4>())
-    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, NUM>(p, pl.tasks, s);
-  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3>())
-    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, NUM>(p, pl.tasks, s);
-  return launch_bf16<KD, NCW, NLW, 2, NUM>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 4, RS>())
+    if (pl.stages == 4) return launch_bf16<KD, NCW, NLW, 4, NUM, RS>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 3, RS>())
+    if (pl.stages == 3) return launch_bf16<KD, NCW, NLW, 3, NUM, RS>(p, pl.tasks, s);
+  if constexpr (cgdr::bf16_config_ok<KD, NCW, NLW, 2, RS>())
+    return launch_bf16<KD, NCW, NLW, 2, NUM, RS>(p, pl.tasks, s);
+  return hipErrorInvalidConfiguration;
 }
 
-template <int KD, int NCW, int NUM>
+template <int KD, int NCW, int NUM, int RS>
 hipError_t dispatch_bf16_nlw(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
-  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, NUM>(p, pl, s);
+  if (pl.nlw == 1) return dispatch_bf16_stages<KD, NCW, 1, NUM, RS>(p, pl, s);
   if constexpr (NUM == 0)
-    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, NUM>(p, pl, s);
-  return dispatch_bf16_stages<KD, NCW, 2, NUM>(p, pl, s);
+    if (pl.nlw == 4) return dispatch_bf16_stages<KD, NCW, 4, NUM, RS>(p, pl, s);
+  return dispatch_bf16_stages<KD, NCW, 2, NUM, RS>(p, pl, s);
 }
 
 template <int KD, int NUM>
 hipError_t dispatch_bf16(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if constexpr (KD == 256) {
-    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, NUM, 1>(p, pl, s);
   } else {
-    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, NUM>(p, pl, s);
-    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, NUM>(p, pl, s);
-    return dispatch_bf16_nlw<KD, 1, NUM>(p, pl, s);
+    if constexpr (KD >= 64) {
+      if (pl.rs == 2) {
+        if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, NUM, 2>(p, pl, s);
+        return dispatch_bf16_nlw<KD, 1, NUM, 2>(p, pl, s);
+      }
+    }
+    if (pl.ncw == 2) return dispatch_bf16_nlw<KD, 2, NUM, 1>(p, pl, s);
+    if (pl.ncw == 4) return dispatch_bf16_nlw<KD, 4, NUM, 1>(p, pl, s);
+    return dispatch_bf16_nlw<KD, 1, NUM, 1>(p, pl, s);
   }
 }
 

@@ -22,13 +22,15 @@
 //
 // Roles inside a workgroup (wave index; the waves of a workgroup are dealt to the CU's four
 // SIMDs in order, so waves w and w+4 share one):
-//   0 .. NCW-1  compute waves, 16 value columns each; no global memory traffic in the loop
-//   NCW .. NCW+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1 from LDS
+//   0 .. NCWT-1  compute waves (NCWT = RS * NCW): 16 value columns each, or with RS = 2 two
+//               waves per 16 columns, each holding half of the state rows; no global memory
+//               traffic in the loop
+//   NCWT .. NCWT+NSW-1  store waves (NSW = NCW): h snapshot and v_new of chunk c-1 from LDS
 //               staging to HBM, store instructions shared round-robin; without helper
 //               workgroups, store wave 0 also touches chunk c+prefetch into L2
-//   NCW+NSW .. NCW+NSW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
+//   NCWT+NSW .. NCWT+NSW+NLW-1  load waves: direct-to-LDS DMA of the W, K, U tiles of chunk
 //               c+STAGES-1 (shared round-robin)
-//   NCW+NSW+NLW gate wave: loads the raw g rows (two chunks ahead, into registers) and
+//   NCWT+NSW+NLW gate wave: loads the raw g rows (two chunks ahead, into registers) and
 //               writes the gate factors of chunk c+1 into LDS
 // With two compute waves the order puts the store waves on SIMDs of their own and the light
 // load and gate waves beside the compute waves (measured: 13 % faster than the store waves
@@ -339,24 +341,31 @@ __device__ __forceinline__ int order_task(const FwdHParams& p, int d) {
 //   NCW     compute waves; Vt = 16 * NCW
 //   NLW     load waves (1, 2 or 4)
 //   STAGES  LDS ring depth (chunks in flight: STAGES - 1 ahead of the compute waves)
+//   RS      compute waves per 16 value columns: 1, or 2 with the state rows split between them
 // =============================================================================================
-template <int KD, int NCW, int NLW, int STAGES>
+template <int KD, int NCW, int NLW, int STAGES, int RS = 1>
 struct Bf16Layout {
   static constexpr int VT = 16 * NCW;
+  static constexpr int NCWT = RS * NCW;            // compute waves
   static constexpr int P = KD / 8;                 // 16-byte pieces per K row
   static constexpr int W_OFF = 0;
   static constexpr int K_OFF = 128 * KD;
   static constexpr int U_OFF = 256 * KD;
   static constexpr int G_OFF = 256 * KD + 128 * VT;            // gamma[64], a
   static constexpr int STAGE_BYTES = ((G_OFF + 260) + 255) / 256 * 256;
-  static constexpr int SS_OFF = STAGES * STAGE_BYTES;          // state staging, 2 buffers
+  static constexpr int SS_BUFS = RS == 1 ? 2 : 3;
+  static constexpr int SS_OFF = STAGES * STAGE_BYTES;          // state staging, SS_BUFS buffers
   static constexpr int SS_BYTES = VT * KD * 2;
-  static constexpr int SV_OFF = SS_OFF + 2 * SS_BYTES;         // v_new staging, 2 buffers
+  static constexpr int SV_OFF = SS_OFF + SS_BUFS * SS_BYTES;   // v_new staging, 2 buffers
   static constexpr int SV_BYTES = VT * kChunk * 2;
-  static constexpr int TRASH_OFF = SV_OFF + 2 * SV_BYTES;      // L2-prefetch landing area
+  static constexpr int XV_OFF = SV_OFF + 2 * SV_BYTES;         // row split: Vd exchange, 1 KiB a wave
+  static constexpr int XV_BYTES = RS == 1 ? 0 : NCWT * 1024;
+  static constexpr int XF_OFF = XV_OFF + XV_BYTES;             // row split: exchange flags
+  static constexpr int XF_BYTES = RS == 1 ? 0 : 256;
+  static constexpr int TRASH_OFF = XF_OFF + XF_BYTES;          // L2-prefetch landing area
   static constexpr int LDS_BYTES = TRASH_OFF + 256;
   static constexpr int NSW = NCW;                              // store waves
-  static constexpr int THREADS = 64 * (NCW + NLW + NSW + 1);
+  static constexpr int THREADS = 64 * (NCWT + NLW + NSW + 1);
   static constexpr int DMA_W = 128 * KD / 1024;               // DMA instructions per tile
   static constexpr int DMA_U = (128 * VT + 1023) / 1024;
   static constexpr int DMA_TILES = 2 * DMA_W + DMA_U;         // per chunk, over all load waves
@@ -370,26 +379,30 @@ struct Bf16Layout {
 
 // A configuration is valid when its LDS fits one gfx950 workgroup (160 KiB) and the prefetch
 // depth D = STAGES - 1 can be awaited with vmcnt (<= 63 outstanding VMEM instructions per
-// wave; load wave 0 carries the most per chunk).
-template <int KD, int NCW, int NLW, int STAGES>
+// wave; load wave 0 carries the most per chunk).  The row split needs an even number of
+// 32-row state blocks (KD >= 64) and at most 8 waves (two per SIMD).
+template <int KD, int NCW, int NLW, int STAGES, int RS = 1>
 constexpr bool bf16_config_ok() {
-  using L = Bf16Layout<KD, NCW, NLW, STAGES>;
+  using L = Bf16Layout<KD, NCW, NLW, STAGES, RS>;
   constexpr int per_chunk = L::template dma_per_chunk<0>();
-  return STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES - 2) * per_chunk <= 63;
+  constexpr bool rs_ok = RS == 1 || (RS == 2 && (KD / 32) % 2 == 0 && L::THREADS <= 512);
+  return rs_ok && STAGES >= 2 && L::LDS_BYTES <= 160 * 1024 && (STAGES - 2) * per_chunk <= 63;
 }
-template <int KD, int NCW, int NLW>
+template <int KD, int NCW, int NLW, int RS = 1>
 constexpr int bf16_max_stages() {
-  return bf16_config_ok<KD, NCW, NLW, 4>() ? 4 : bf16_config_ok<KD, NCW, NLW, 3>() ? 3 : 2;
+  return bf16_config_ok<KD, NCW, NLW, 4, RS>() ? 4 : bf16_config_ok<KD, NCW, NLW, 3, RS>() ? 3
+                                                                                          : bf16_config_ok<KD, NCW, NLW, 2, RS>() ? 2 : 0;
 }
 
 // NUM: 0 default numerics; 1 contest, fast pass (plain fp16 roundings, flags the heads where a
 // saturating cast or nan_to_num could matter); 2 contest, full pass (the saturating casts, only
 // for flagged heads).
-template <int KD, int NCW, int NLW, int STAGES, int NUM = 0>
-__global__ void __launch_bounds__(64 * (NCW + NLW + NCW + 1))
+template <int KD, int NCW, int NLW, int STAGES, int NUM = 0, int RS = 1>
+__global__ void __launch_bounds__(64 * (RS * NCW + NLW + NCW + 1))
 cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
   constexpr bool CONTEST = NUM != 0, FULL = NUM == 2;
-  using L = Bf16Layout<KD, NCW, NLW, STAGES>;
+  using L = Bf16Layout<KD, NCW, NLW, STAGES, RS>;
+  constexpr int NCWT = L::NCWT;
   constexpr int VT = L::VT, P = L::P;
   constexpr int KT = KD / 16;   // MM2 output tiles (rows of S)
   constexpr int KB = KD / 32;   // MM1 contraction blocks
@@ -559,7 +572,281 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     return;
   }
 
-  if (wave < NCW) {
+  if (wave < NCWT) {
+   if constexpr (RS == 2) {
+    // ------------------------------------------------------------------ compute waves, rows split
+    // Wave (j, r) = (wave / 2, wave % 2) owns value columns 16 j .. 16 j + 15 of the tile and the
+    // state rows of MM2 tiles kt = KT/2 r .. KT/2 r + KT/2 - 1 (k = KD/2 r .. KD/2 r + KD/2 - 1).
+    // MM1 for token block tb = r takes the whole bf16(-S) of its columns, its own rows and its
+    // partner's, from the staging buffer the store waves read for the h snapshot (three buffers:
+    // bf16(-S) of chunk c+1 is staged at the end of chunk c).  MM2 of its rows needs Vd of both
+    // token blocks, so the two partners swap Vd through LDS once per chunk (1 KiB each, with a
+    // flag).  Each wave reads half of the W and K^T operands and does half of the MFMA and VALU
+    // work of a wave that owns all rows; every accumulation chain runs in the same order
+    // (MM1: U, then k-blocks 0, 1, ...; MM2: a S, then token block 0, then 1), so the results
+    // are bit-identical to that layout.
+    constexpr int KTH = KT / 2, KBH = KB / 2;
+    const int j = wave >> 1, r = wave & 1;
+    const int g = lane >> 4, n = lane & 15;
+    const int e = n >> 2, q = n & 3;
+    const int vcol = vbase + 16 * j + n;         // value column owned by this lane
+    const int vrow = 16 * j + n;                 // its row in the staging buffers
+    // state element (i, rr) of this wave: own tile kt = KTH r + i, k row krow(i, rr)
+    auto krow_of = [&](int i, int rr) { return 32 * (KBH * r + (i >> 1)) + 8 * g + 4 * (i & 1) + rr; };
+    f32x4 S[KTH];
+    if (p.h0 != nullptr) {
+      const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
+#pragma unroll
+      for (int i = 0; i < KTH; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int krow = krow_of(i, rr);
+          const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
+          S[i][rr] = krow >= p.K ? 0.f
+                     : p.h0_f32 ? ((const float*)p.h0)[off]
+                                : bf16_lo(((const unsigned short*)p.h0)[off]);
+          if constexpr (CONTEST) S[i][rr] = bf16_rnd(S[i][rr]);   // the state is bf16
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KTH; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // byte offsets of the staged pieces (vrow, k-block kb) of bf16(-S): all k-blocks (MM1
+    // operands), and this wave's own ones (where it stages its rows)
+    int soff[KB], sown[KBH];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) soff[kb] = (vrow * P + ((4 * kb + g) ^ swz_s<P>(vrow))) * 16;
+#pragma unroll
+    for (int ib = 0; ib < KBH; ++ib) sown[ib] = (vrow * P + ((4 * (KBH * r + ib) + g) ^ swz_s<P>(vrow))) * 16;
+    // K^T operand pieces of own k-block ib: the swizzle of row 32 tb + 8 g + 4 half + e depends
+    // only on the row's two low bits, which are e's
+    int kofs[KBH];
+#pragma unroll
+    for (int ib = 0; ib < KBH; ++ib) kofs[ib] = ((4 * (KBH * r + ib) + q) ^ swz_k<P>(8 * g + e)) * 16;
+    auto stage_state = [&](int buf) {
+      char* ss = smem + L::SS_OFF + buf * L::SS_BYTES;
+#pragma unroll
+      for (int ib = 0; ib < KBH; ++ib) {
+        u32x4 w;
+        w[0] = pack_bf16x2(-S[2 * ib][0], -S[2 * ib][1]);
+        w[1] = pack_bf16x2(-S[2 * ib][2], -S[2 * ib][3]);
+        w[2] = pack_bf16x2(-S[2 * ib + 1][0], -S[2 * ib + 1][1]);
+        w[3] = pack_bf16x2(-S[2 * ib + 1][2], -S[2 * ib + 1][3]);
+        *(u32x4*)(ss + sown[ib]) = w;
+      }
+    };
+    char* const xme = smem + L::XV_OFF + ((2 * j + r) * 64 + lane) * 16;
+    const char* const xpa = smem + L::XV_OFF + ((2 * j + (r ^ 1)) * 64 + lane) * 16;
+    typedef __attribute__((address_space(3))) int lds_int;
+    volatile lds_int* const fme = (volatile lds_int*)((lds_char*)smem + L::XF_OFF) + 2 * j + r;
+    volatile lds_int* const fpa = (volatile lds_int*)((lds_char*)smem + L::XF_OFF) + 2 * j + (r ^ 1);
+    if (lane == 0) *fme = 0;
+    stage_state(0);
+    block_barrier();   // P: stage 0 ready, bf16(-S_0) staged, flags cleared
+
+    auto chunk_step = [&](const int c, auto st_tag, auto par_tag) {
+      constexpr int st = decltype(st_tag)::value;
+      constexpr int par = decltype(par_tag)::value;
+      const char* sbase = smem + st * L::STAGE_BYTES;
+      const lds_char* stage = (const lds_char*)sbase;
+      const float* gam = (const float*)(sbase + L::G_OFF);
+      const char* ssr = smem + L::SS_OFF + (c % 3) * L::SS_BYTES;   // bf16(-S_c)
+
+      // Phase 1: the LDS reads of MM1 and the epilogue (token block r): a, gamma, U, W, bf16(-S).
+      const float a = gam[64];
+      f32x4 gm[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) gm[hh] = *(const f32x4*)(gam + 32 * r + 8 * g + 4 * hh);
+      u32x2 uraw[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int t0 = 32 * r + 8 * g + 4 * hh;
+        const lds_char* up = stage + L::U_OFF + ((t0 + e) * VT + 16 * j + 4 * q) * 2;
+        uraw[hh] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)up));
+      }
+      u32x4 wop[2][KB];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int row = 32 * r + 8 * e + 4 * hh + q;
+        const u32x4* wrow = (const u32x4*)(sbase + L::W_OFF) + row * P;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) wop[hh][kb] = wrow[(4 * kb + g) ^ swz_w<P>(row)];
+      }
+      u32x4 Sw[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) Sw[kb] = *(const u32x4*)(ssr + soff[kb]);
+      f32x4 acc[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        acc[hh] = CONTEST ? f32x4{0.f, 0.f, 0.f, 0.f}
+                          : f32x4{bf16_lo(uraw[hh][0]), bf16_hi(uraw[hh][0]), bf16_lo(uraw[hh][1]), bf16_hi(uraw[hh][1])};
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Phase 2: MM1 of token block r (two chains, k-block major), the decay of own rows and the
+      // K^T reads of token block 0 between the MFMAs.
+      auto read_kop = [&](int tb, u32x4* kop) {
+#pragma unroll
+        for (int i = 0; i < KTH; ++i) {
+#pragma unroll
+          for (int half = 0; half < 2; ++half) {
+            const int row = 32 * tb + 8 * g + 4 * half + e;
+            const lds_char* kp = stage + L::K_OFF + row * P * 16 + kofs[i >> 1] + 8 * (i & 1);
+            const u32x2 kw = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)kp));
+            kop[i][2 * half] = kw[0];
+            kop[i][2 * half + 1] = kw[1];
+          }
+        }
+      };
+      u32x4 kop0[KTH], kop1[KTH];
+      unsigned hdp[CONTEST ? KTH : 1][2];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+          acc[hh] = mfma_bf16(__builtin_bit_cast(bf16x8, wop[hh][kb]), __builtin_bit_cast(bf16x8, Sw[kb]), acc[hh]);
+#pragma unroll
+      for (int i = 0; i < KTH; ++i) {
+        if constexpr (FULL) {
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr)
+            hdp[i][rr] = pack_bf16x2(f16_sat(f16_sat(S[i][2 * rr]) * a), f16_sat(f16_sat(S[i][2 * rr + 1]) * a));
+          S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (CONTEST) {
+          const h16x2 a16 = to_h16x2(a, a);
+#pragma unroll
+          for (int rr = 0; rr < 2; ++rr)
+            hdp[i][rr] = h16x2_to_bf16x2(to_h16x2(S[i][2 * rr], S[i][2 * rr + 1]) * a16);
+          S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+          S[i] = S[i] * a;
+        }
+      }
+      read_kop(0, kop0);
+#pragma unroll
+      for (int i = 0; i < 2 * KB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, (KTH + 2 * KB - 1) / (2 * KB), 0);   // VALU
+        __builtin_amdgcn_sched_group_barrier(0x100, (2 * KTH + 2 * KB - 1) / (2 * KB), 0);   // DS read
+      }
+      __builtin_amdgcn_sched_barrier(0);
+
+      // Phase 3: epilogue of token block r (v_new staging, Vd), Vd to the partner.
+      u32x4 pv, pd;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int hh = jj >> 1, rr = 2 * (jj & 1);
+        const float v0 = acc[hh][rr], v1 = acc[hh][rr + 1];
+        if constexpr (CONTEST) {
+          const u32x2 ur = uraw[hh];
+          const float u0 = rr == 0 ? bf16_lo(ur[0]) : bf16_lo(ur[1]);
+          const float u1 = rr == 0 ? bf16_hi(ur[0]) : bf16_hi(ur[1]);
+          if constexpr (FULL) {
+            const float x0 = f16_sat(f16_sat(u0) - f16_nan_to_num(-bf16_rnd(v0)));
+            const float x1 = f16_sat(f16_sat(u1) - f16_nan_to_num(-bf16_rnd(v1)));
+            pv[jj] = pack_bf16x2(x0, x1);
+            pd[jj] = pack_bf16x2(f16_sat(x0 * gm[hh][rr]), f16_sat(x1 * gm[hh][rr + 1]));
+          } else {
+            const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(v0, v1));
+            pv[jj] = h16x2_to_bf16x2(x16);
+            pd[jj] = h16x2_to_bf16x2(x16 * to_h16x2(gm[hh][rr], gm[hh][rr + 1]));
+          }
+        } else {
+          pv[jj] = pack_bf16x2(v0, v1);
+          pd[jj] = pack_bf16x2(v0 * gm[hh][rr], v1 * gm[hh][rr + 1]);
+        }
+      }
+      {
+        u32x4* sv = (u32x4*)(smem + L::SV_OFF + par * L::SV_BYTES);
+        sv[vrow * 8 + ((4 * r + g) ^ swz_v(vrow))] = pv;
+      }
+      *(u32x4*)xme = pd;
+      // the Vd write has landed before the flag is raised (LDS ops of a wave complete in order,
+      // and lgkmcnt(0) waits for them)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) *fme = c + 1;
+      read_kop(1, kop1);
+      // The partner raises its flag to c + 1 once its Vd of chunk c is in LDS.  It cannot be a
+      // chunk ahead: it writes chunk c+1's Vd and flag only after barrier B_c, which this wave
+      // reaches after reading.  The bound on the polls only guarantees an exit.
+      auto partner_vd = [&]() -> bf16x8 {
+        for (int it = 0; it < (1 << 20); ++it)
+          if (__builtin_amdgcn_readfirstlane(*fpa) >= c + 1) break;
+        asm volatile("" ::: "memory");
+        return __builtin_bit_cast(bf16x8, *(const u32x4*)xpa);
+      };
+
+      // Phase 4: MM2 of own rows, token block 0 then 1 (the order of the one-wave layout).
+      bf16x8 Vd1;
+      if (r == 0) {
+        const bf16x8 Vd0 = __builtin_bit_cast(bf16x8, pd);
+#pragma unroll
+        for (int i = 0; i < KTH; ++i) S[i] = mfma_bf16(__builtin_bit_cast(bf16x8, kop0[i]), Vd0, S[i]);
+        Vd1 = partner_vd();
+      } else {
+        const bf16x8 Vd0 = partner_vd();
+#pragma unroll
+        for (int i = 0; i < KTH; ++i) S[i] = mfma_bf16(__builtin_bit_cast(bf16x8, kop0[i]), Vd0, S[i]);
+        Vd1 = __builtin_bit_cast(bf16x8, pd);
+      }
+#pragma unroll
+      for (int i = 0; i < KTH; ++i) S[i] = mfma_bf16(__builtin_bit_cast(bf16x8, kop1[i]), Vd1, S[i]);
+      if constexpr (CONTEST) {
+#pragma unroll
+        for (int i = 0; i < KTH; ++i) {
+          if constexpr (FULL) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const unsigned hw = hdp[i][rr >> 1];
+              const float hd = (rr & 1) ? bf16_hi(hw) : bf16_lo(hw);
+              S[i][rr] = bf16_rnd(hd + bf16_rnd(f16_nan_to_num(bf16_rnd(S[i][rr]))));
+            }
+          } else {
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr) {
+              const unsigned upk = h16x2_to_bf16x2(bf16x2_to_h16x2(pack_bf16x2(S[i][2 * rr], S[i][2 * rr + 1])));
+              const unsigned hw = hdp[i][rr];
+              const unsigned sw = pack_bf16x2(bf16_lo(hw) + bf16_lo(upk), bf16_hi(hw) + bf16_hi(upk));
+              S[i][2 * rr] = bf16_lo(sw);
+              S[i][2 * rr + 1] = bf16_hi(sw);
+            }
+          }
+        }
+      }
+      stage_state((c + 1) % 3);   // bf16(-S_{c+1}): MM1 of chunk c+1 and the h snapshot
+      wait_lgkm0();
+      block_barrier();   // B_c
+    };
+    constexpr int UNROLL = (STAGES % 2 == 0) ? STAGES : 2 * STAGES;
+    for (int c0 = 0; c0 < NC; c0 += UNROLL) {
+      static_for<0, UNROLL>([&](auto i) {
+        constexpr int I = decltype(i)::value;
+        if (c0 + I < NC)
+          chunk_step(c0 + I, std::integral_constant<int, I % STAGES>{}, std::integral_constant<int, I % 2>{});
+      });
+    }
+
+    if constexpr (NUM == 1) {
+      bool bad = false;
+#pragma unroll
+      for (int i = 0; i < KTH; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) bad |= S[i][rr] != S[i][rr];
+      if (__any(bad) && lane == 0) p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
+    }
+    if (p.final_state != nullptr) {
+      const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
+#pragma unroll
+      for (int i = 0; i < KTH; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int krow = krow_of(i, rr);
+          const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
+          if (krow >= p.K) continue;
+          if (p.final_f32) ((float*)p.final_state)[off] = S[i][rr];
+          else ((__bf16*)p.final_state)[off] = (__bf16)S[i][rr];
+        }
+    }
+   } else {
     // ------------------------------------------------------------------ compute wave
     const int g = lane >> 4, n = lane & 15;
     const int vcol = vbase + 16 * wave + n;      // value column owned by this lane
@@ -813,12 +1100,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
         }
     }
-  } else if (wave >= NCW + L::NSW && wave < NCW + L::NSW + NLW) {
+   }
+  } else if (wave >= NCWT + L::NSW && wave < NCWT + L::NSW + NLW) {
     // ------------------------------------------------------------------ load waves
     // The tile DMAs of a chunk are dealt round-robin over the NLW load waves (instruction
     // i goes to wave i % NLW), so each wave's vmcnt covers only its share and more loads are
     // in flight per CU.  The g rows are not theirs: the gate wave loads them into registers.
-    const int lw = wave - NCW - L::NSW;
+    const int lw = wave - NCWT - L::NSW;
     const __bf16* kbase = (const __bf16*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
     const __bf16* wbase = (const __bf16*)p.w + tk.b * p.sw_b + (int64_t)tk.head * p.sw_h;
     const __bf16* ubase = (const __bf16*)p.u + tk.b * p.su_b + (int64_t)tk.head * p.su_h + vbase;
@@ -963,12 +1251,12 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       else if (lw == 2) run_loader(std::integral_constant<int, 2>{});
       else run_loader(std::integral_constant<int, 3>{});
     }
-  } else if (wave >= NCW && wave < NCW + L::NSW) {
+  } else if (wave >= NCWT && wave < NCWT + L::NSW) {
     // ------------------------------------------------------------------ store waves
     // h snapshot and v_new of a chunk, from the LDS staging buffers: each 16-lane block takes
     // units of (16 rows x 8 value columns); two transposed reads give a lane 8 consecutive
     // value columns of one row, stored as one 16-byte write.
-    const int sw = wave - NCW;   // this store wave takes store instructions m % NSW == sw
+    const int sw = wave - NCWT;   // this store wave takes store instructions m % NSW == sw
     const int blk = lane >> 4, i = lane & 15;
     const int e = i >> 2, q = i & 3;
     __bf16* hbase = (__bf16*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h + vbase;
@@ -979,51 +1267,71 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     // both hold when no bf16 exceeds 65280 (0x477f): the next bf16 is 65536.
     unsigned amax = 0;
 
-    auto store_chunk = [&](int c) {
+    // One chunk's stores; SW (this store wave's index, a compile-time constant) selects its
+    // share: h instruction m when m % NSW == SW, v_new instruction m when (MH + m) % NSW == SW.
+    // All of the share's LDS reads are issued first and awaited once, then the stores.
+    auto store_chunk = [&](int c, auto sw_tag) {
+      constexpr int SW = decltype(sw_tag)::value;
+      constexpr int UNITS_H = (KD / 16) * (VT / 8), MH = UNITS_H / 4;   // 16-byte row stores of h
+      constexpr int UNITS_V = 4 * (VT / 8), MV = UNITS_V / 4;           // and of v_new
       const int len = (int)((tk.len - (int64_t)c * kChunk) < kChunk ? (tk.len - (int64_t)c * kChunk) : kChunk);
-      const char* ss = smem + L::SS_OFF + (c & 1) * L::SS_BYTES;
-      __bf16* hdst = hbase + (tk.boh + c) * p.sh_c;
-      constexpr int UNITS_H = (KD / 16) * (VT / 8);
+      const char* ss = smem + L::SS_OFF + (RS == 1 ? (c & 1) : c % 3) * L::SS_BYTES;
+      const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
+      const bool with_v = vbase_ptr != nullptr || NUM == 1;
+      u32x2 hx[MH][2], vx[MV][2];
 #pragma unroll
-      for (int m = 0; m < UNITS_H / 4; ++m) {
-        if (m % L::NSW != sw) continue;
+      for (int m = 0; m < MH; ++m) {
+        if (m % L::NSW != SW) continue;
         const int unit = 4 * m + blk;
         const int k0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
         const int kk = k0 + 4 * q;
-        u32x4 hv;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
           const int vrow = v0 + 4 * half + e;
           const int piece = (kk >> 3) ^ swz_s<P>(vrow);
           const lds_char* sp = (const lds_char*)ss + (vrow * P + piece) * 16 + 8 * ((kk >> 2) & 1);
-          const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
-          hv[2 * half] = x[0] ^ 0x80008000u;       // staged as bf16(-S)
-          hv[2 * half + 1] = x[1] ^ 0x80008000u;
-          if constexpr (NUM == 1) amax = pk_absmax_bf16(pk_absmax_bf16(amax, x[0]), x[1]);
+          hx[m][half] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
         }
-        if (k0 < p.K) *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;   // rows >= K: padding
       }
-      if (vbase_ptr != nullptr || NUM == 1) {
-        const char* sv = smem + L::SV_OFF + (c & 1) * L::SV_BYTES;
-        __bf16* vdst = vbase_ptr == nullptr ? nullptr : vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
-        constexpr int UNITS_V = 4 * (VT / 8);
+      if (with_v) {
 #pragma unroll
-        for (int m = 0; m < (UNITS_V + 3) / 4; ++m) {
-          if ((UNITS_H / 4 + m) % L::NSW != sw) continue;
+        for (int m = 0; m < MV; ++m) {
+          if ((MH + m) % L::NSW != SW) continue;
           const int unit = 4 * m + blk;
-          if (UNITS_V % 4 != 0 && unit >= UNITS_V) break;
           const int t0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
           const int tt = t0 + 4 * q;
-          u32x4 vv;
 #pragma unroll
           for (int half = 0; half < 2; ++half) {
             const int vrow = v0 + 4 * half + e;
             const int piece = (tt >> 3) ^ swz_v(vrow);
             const lds_char* sp = (const lds_char*)sv + (vrow * 8 + piece) * 16 + 8 * ((tt >> 2) & 1);
-            const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
-            vv[2 * half] = x[0];
-            vv[2 * half + 1] = x[1];
+            vx[m][half] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)sp));
           }
+        }
+      }
+      __bf16* hdst = hbase + (tk.boh + c) * p.sh_c;
+#pragma unroll
+      for (int m = 0; m < MH; ++m) {
+        if (m % L::NSW != SW) continue;
+        const int unit = 4 * m + blk;
+        const int k0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
+        u32x4 hv;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          hv[2 * half] = hx[m][half][0] ^ 0x80008000u;       // staged as bf16(-S)
+          hv[2 * half + 1] = hx[m][half][1] ^ 0x80008000u;
+          if constexpr (NUM == 1) amax = pk_absmax_bf16(pk_absmax_bf16(amax, hx[m][half][0]), hx[m][half][1]);
+        }
+        if (k0 < p.K) *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;   // rows >= K: padding
+      }
+      if (with_v) {
+        __bf16* vdst = vbase_ptr == nullptr ? nullptr : vbase_ptr + (tk.bos + (int64_t)c * kChunk) * p.sv_t;
+#pragma unroll
+        for (int m = 0; m < MV; ++m) {
+          if ((MH + m) % L::NSW != SW) continue;
+          const int unit = 4 * m + blk;
+          const int t0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
+          const u32x4 vv = {vx[m][0][0], vx[m][0][1], vx[m][1][0], vx[m][1][1]};
           if (t0 + i < len) {
             if (vbase_ptr != nullptr) *(u32x4*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = vv;
             if constexpr (NUM == 1)
@@ -1044,22 +1352,33 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     if (touching) l2_touch_setup();
     for (int j = 1; j < pf; ++j) prefetch(j);
     block_barrier();   // P
-    for (int c = 0; c < NC; ++c) {
-      prefetch(c + pf);
-      if (c >= 1) store_chunk(c - 1);
-      wait_lgkm0();
-      block_barrier();   // B_c
-      if (p.helpers && sw == 0 && lane == 0)
-        __hip_atomic_store(p.progress + task_id * kProgressStride,
-                           (int)(((unsigned)p.epoch << 24) | (unsigned)(c + 1)), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+    auto run_stores = [&](auto sw_tag) {
+      constexpr int SW = decltype(sw_tag)::value;
+      for (int c = 0; c < NC; ++c) {
+        prefetch(c + pf);
+        if (c >= 1) store_chunk(c - 1, sw_tag);
+        wait_lgkm0();
+        block_barrier();   // B_c
+        if (SW == 0 && p.helpers && lane == 0)
+          __hip_atomic_store(p.progress + task_id * kProgressStride,
+                             (int)(((unsigned)p.epoch << 24) | (unsigned)(c + 1)), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (NC > 0) store_chunk(NC - 1, sw_tag);
+    };
+    if (sw == 0) run_stores(std::integral_constant<int, 0>{});
+    else if constexpr (L::NSW >= 2) {
+      if (sw == 1) run_stores(std::integral_constant<int, 1>{});
+      else if constexpr (L::NSW == 4) {
+        if (sw == 2) run_stores(std::integral_constant<int, 2>{});
+        else run_stores(std::integral_constant<int, 3>{});
+      }
     }
-    if (NC > 0) store_chunk(NC - 1);
     if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
     if constexpr (NUM == 1)
       if (__any((amax & 0xffffu) > 0x477fu || (amax >> 16) > 0x477fu) && lane == 0)
         p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
-  } else if (wave == NCW + L::NSW + NLW) {
+  } else if (wave == NCWT + L::NSW + NLW) {
     // ------------------------------------------------------------------ gate wave
     // Loads the raw g rows itself, with ordinary loads into registers two chunks ahead, and
     // turns them into the gate factors of chunk c+1 during iteration c (read by the compute

@@ -55,8 +55,8 @@ int main(void) {
   F(cgdr_fwd_h_args, stride_h0); F(cgdr_fwd_h_args, stride_final); F(cgdr_fwd_h_args, tuning);
   F(cgdr_fwd_h_args, state_layout); F(cgdr_fwd_h_args, reserved);
   F(cgdr_fwd_h_plan, lds_bytes); F(cgdr_fwd_h_plan, workgroups); F(cgdr_fwd_h_plan, helpers);
-  F(cgdr_fwd_h_plan, xcd_count);
-  F(cgdr_fwd_h_tuning, helpers); F(cgdr_fwd_h_tuning, cu_count); F(cgdr_fwd_h_tuning, reserved);
+  F(cgdr_fwd_h_plan, xcd_count); F(cgdr_fwd_h_plan, row_split);
+  F(cgdr_fwd_h_tuning, helpers); F(cgdr_fwd_h_tuning, cu_count); F(cgdr_fwd_h_tuning, row_split);
   printf("tuning %zu\n", sizeof(cgdr_fwd_h_tuning));
   return 0;
 }''')
@@ -328,7 +328,7 @@ def test_tuning_overrides_and_rejections(lib):
     p = _abi.get_plan(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128,
                             tuning=dict(cu_count=256, xcd_count=8, load_waves=1, stages=2)))
     assert (p.load_waves, p.stages) == (1, 2)
-    for bad in (dict(v_tile=48), dict(helpers=2), dict(load_waves=3), dict(stages=5), dict(reserved=1),
+    for bad in (dict(v_tile=48), dict(helpers=2), dict(load_waves=3), dict(stages=5), dict(row_split=3),
                 dict(cu_count=-1)):
         a = _args(tuning=bad)
         assert _status(a)[0] == _abi.CGDR_ERR_INVALID, bad

@@ -291,6 +291,42 @@ def test_vtile_and_depth_invariance(dev):
                 assert torch.equal(a, b), (key, val)
 
 
+@pytest.mark.parametrize("K,V,numerics", [(128, 128, 0), (64, 64, 0), (100, 128, 0), (48, 64, 0),
+                                           (128, 128, 1), (64, 96, 1), (100, 100, 1)])
+def test_row_split_is_bit_identical(dev, K, V, numerics):
+    """Two compute waves per 16 value columns, each with half of the state rows (row_split=2),
+    against one wave with all rows (row_split=1): bit-identical h, v_new and final state, under
+    16- and 32-column tiles, helpers on and off, every pipeline depth; grouped heads, an initial
+    state, a packed batch with partial chunks.  For the contest numerics one head holds u
+    beyond the fp16 range, so that its full pass (the saturating casts) runs as well."""
+    cu = np.array([0, 130, 330, 391], np.int64)
+    if numerics == 0:
+        inp = _case(70 + K, 1, 391, 4, K, V, Hg=2, gate="linear", cu=cu, profile="golden")
+        d = dev_inputs(inp, torch.bfloat16, dev)
+        call = lambda tu: abi_call(d, tuning=tu)
+    else:
+        inp = _case(70 + K, 1, 391, 4, K, V, Hg=2, gate="linear", cu=cu, profile="golden")
+        inp["initial_state"] = O.bf16_round(inp["initial_state"])
+        inp["u"] = inp["u"].copy()
+        inp["u"][0, 140:150, 1] *= 1.2e5          # head 1: u beyond the fp16 range (full pass)
+        d = dev_inputs(inp, torch.bfloat16, dev, h0_dtype=torch.bfloat16)
+        call = lambda tu: abi_call(d, tuning=tu, numerics=1, final_dtype=torch.bfloat16)
+    base = call(dict(row_split=1))
+    for tu in (dict(), dict(v_tile=16), dict(v_tile=32, helpers=1), dict(v_tile=16, stages=2),
+               dict(v_tile=32, stages=2), dict(v_tile=16, load_waves=1), dict(v_tile=16, stages=4)):
+        if V % tu.get("v_tile", 16):
+            continue
+        out = call(dict(tu, row_split=2))
+        for name, a, b in zip(("h", "v_new", "final"), base, out):
+            assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                               b.view(torch.int16) if b.dtype == torch.bfloat16 else b), (tu, name)
+    if numerics == 1:   # and the contest model itself
+        ref = O.fwd_h_o2(inp["k"], np.swapaxes(inp["w"], 1, 2).copy(), np.swapaxes(inp["u"], 1, 2).copy(),
+                         np.swapaxes(inp["g"], 1, 2).copy(), inp["initial_state"], cu)
+        got_v = np.swapaxes(np32(base[1]), 1, 2)
+        assert ((got_v == ref[1]) | (np.isnan(got_v) & np.isnan(ref[1]))).mean() >= 0.985
+
+
 def test_wide_value_vtile_invariance(dev):
     """Config 4's V = 256 under every V-tile the plan offers (16, 32 and 64 columns; the default
     plan takes 32): bit-identical outputs."""
