@@ -204,6 +204,22 @@ __device__ __forceinline__ unsigned h16x2_to_bf16x2(h16x2 x) {
   const f32x2 f = __builtin_convertvector(x, f32x2);
   return pack_bf16x2(f[0], f[1]);
 }
+// The value unchanged, but opaque to the optimizer: it keeps a packed bf16 pair as one word
+// (one v_cvt_pk_bf16_f32 and two unpacks), instead of re-deriving each half with a rounding of
+// its own, and it pins a value computed in one phase of the chunk to that phase.
+__device__ __forceinline__ unsigned opaque(unsigned x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// Contest fast-pass state combine of one pair: bf16(hd + up) with up = bf16(fp16(bf16(x))) of
+// the MFMA sums x.  The fp16 value of a bf16 has at most 8 significant bits, so its float value
+// is already up; the sum is rounded once to bf16 (as the reference's bf16 addition does).
+__device__ __forceinline__ unsigned contest_combine_pair(float x0, float x1, unsigned hd) {
+  const unsigned b = opaque(pack_bf16x2(x0, x1));
+  const f32x2 up = __builtin_convertvector(to_h16x2(bf16_lo(b), bf16_hi(b)), f32x2);
+  return opaque(pack_bf16x2(bf16_lo(hd) + up[0], bf16_hi(hd) + up[1]));
+}
+
 // Running maximum of |x| over the two bf16 of a word, per half (v_pk_max_u16): the bits of
 // |x| order like |x| as unsigned integers, and every NaN lies above +inf (0x7f80).
 __device__ __forceinline__ unsigned pk_absmax_bf16(unsigned acc, unsigned w) {
@@ -715,7 +731,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           const h16x2 a16 = to_h16x2(a, a);
 #pragma unroll
           for (int rr = 0; rr < 2; ++rr)
-            hdp[i][rr] = h16x2_to_bf16x2(to_h16x2(S[i][2 * rr], S[i][2 * rr + 1]) * a16);
+            hdp[i][rr] = opaque(h16x2_to_bf16x2(to_h16x2(S[i][2 * rr], S[i][2 * rr + 1]) * a16));
           S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[i] = S[i] * a;
@@ -803,9 +819,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           } else {
 #pragma unroll
             for (int rr = 0; rr < 2; ++rr) {
-              const unsigned upk = h16x2_to_bf16x2(bf16x2_to_h16x2(pack_bf16x2(S[i][2 * rr], S[i][2 * rr + 1])));
-              const unsigned hw = hdp[i][rr];
-              const unsigned sw = pack_bf16x2(bf16_lo(hw) + bf16_lo(upk), bf16_hi(hw) + bf16_hi(upk));
+              const unsigned sw = contest_combine_pair(S[i][2 * rr], S[i][2 * rr + 1], hdp[i][rr]);
               S[i][2 * rr] = bf16_lo(sw);
               S[i][2 * rr + 1] = bf16_hi(sw);
             }
@@ -972,7 +986,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           const h16x2 a16 = to_h16x2(a, a);
 #pragma unroll
           for (int r = 0; r < 2; ++r)
-            hdp[kt][r] = h16x2_to_bf16x2(to_h16x2(S[kt][2 * r], S[kt][2 * r + 1]) * a16);
+            hdp[kt][r] = opaque(h16x2_to_bf16x2(to_h16x2(S[kt][2 * r], S[kt][2 * r + 1]) * a16));
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[kt] = S[kt] * a;
@@ -1058,9 +1072,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           } else {
 #pragma unroll
             for (int r = 0; r < 2; ++r) {
-              const unsigned up = h16x2_to_bf16x2(bf16x2_to_h16x2(pack_bf16x2(S[kt][2 * r], S[kt][2 * r + 1])));
-              const unsigned hw = hdp[kt][r];
-              const unsigned sw = pack_bf16x2(bf16_lo(hw) + bf16_lo(up), bf16_hi(hw) + bf16_hi(up));
+              const unsigned sw = contest_combine_pair(S[kt][2 * r], S[kt][2 * r + 1], hdp[kt][r]);
               S[kt][2 * r] = bf16_lo(sw);
               S[kt][2 * r + 1] = bf16_hi(sw);
             }
