@@ -211,21 +211,47 @@ __device__ __forceinline__ unsigned opaque(unsigned x) {
   asm volatile("" : "+v"(x));
   return x;
 }
-// Contest fast-pass state combine of one pair: bf16(hd + up) with up = bf16(fp16(bf16(x))) of
-// the MFMA sums x.  The fp16 value of a bf16 has at most 8 significant bits, so its float value
-// is already up; the sum is rounded once to bf16 (as the reference's bf16 addition does).
-__device__ __forceinline__ unsigned contest_combine_pair(float x0, float x1, unsigned hd) {
+__device__ __forceinline__ float opaque_f(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+// c + the fp16 value in the low (high) half of h, in float32 (v_fma_mix_f32 with a factor of 1:
+// one rounding, i.e. the float32 sum; it reads the fp16 operand without a conversion).
+__device__ __forceinline__ float add_f16lo(h16x2 h, float c) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(c));
+  return d;
+}
+__device__ __forceinline__ float add_f16hi(h16x2 h, float c) {
+  float d;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(c));
+  return d;
+}
+// Contest fast pass, state decay of one pair of the bf16 state (packed): bf16(fp16(fp16(S) a16))
+// as two floats, pinned to the phase that computes them.
+__device__ __forceinline__ void contest_decay_pair(unsigned sp, h16x2 a16, float& hd0, float& hd1) {
+  const f32x2 f = __builtin_convertvector(to_h16x2(bf16_lo(sp), bf16_hi(sp)) * a16, f32x2);
+  const unsigned hw = opaque(pack_bf16x2(f[0], f[1]));
+  hd0 = opaque_f(bf16_lo(hw));
+  hd1 = opaque_f(bf16_hi(hw));
+}
+// Contest fast pass, state combine of one pair: bf16(hd + up), packed, with up = bf16(fp16(bf16(x)))
+// of the MFMA sums x.  The fp16 value of a bf16 has at most 8 significant bits, so it is already
+// up; the float32 sum is rounded once to bf16 (as the reference's bf16 addition does).
+__device__ __forceinline__ unsigned contest_combine_pair(float x0, float x1, float hd0, float hd1) {
   const unsigned b = opaque(pack_bf16x2(x0, x1));
-  const f32x2 up = __builtin_convertvector(to_h16x2(bf16_lo(b), bf16_hi(b)), f32x2);
-  return opaque(pack_bf16x2(bf16_lo(hd) + up[0], bf16_hi(hd) + up[1]));
+  const h16x2 up = to_h16x2(bf16_lo(b), bf16_hi(b));
+  return opaque(pack_bf16x2(add_f16lo(up, hd0), add_f16hi(up, hd1)));
 }
 
-// Running maximum of |x| over the two bf16 of a word, per half (v_pk_max_u16): the bits of
-// |x| order like |x| as unsigned integers, and every NaN lies above +inf (0x7f80).
+// Running maximum of |x| over the two bf16 of a word, per half, in one instruction: the bit
+// patterns are read as fp16 and v_pk_maximum3_f16 takes max(acc, x, -x).  Magnitude bit patterns
+// order like the values they encode in either format, and the patterns at or above 0x7c00
+// (bf16 values from 2^121 up, infinities and NaNs) are fp16 infinities and NaNs, which this
+// maximum propagates, so they end up above any finite threshold too.
 __device__ __forceinline__ unsigned pk_absmax_bf16(unsigned acc, unsigned w) {
-  typedef __attribute__((ext_vector_type(2))) unsigned short u16x2;
-  return __builtin_bit_cast(unsigned, __builtin_elementwise_max(__builtin_bit_cast(u16x2, acc),
-                                                                __builtin_bit_cast(u16x2, w & 0x7fff7fffu)));
+  asm("v_pk_maximum3_f16 %0, %0, %1, %1 neg_lo:[0,0,1] neg_hi:[0,0,1]" : "+v"(acc) : "v"(w));
+  return acc;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -627,6 +653,14 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
       for (int i = 0; i < KTH; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // contest fast pass: the bf16 state kept as packed pairs between chunks (S holds only the
+    // MFMA sums of a chunk)
+    unsigned Sp[NUM == 1 ? KTH : 1][2];
+    if constexpr (NUM == 1)
+#pragma unroll
+      for (int i = 0; i < KTH; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) Sp[i][rr] = pack_bf16x2(S[i][2 * rr], S[i][2 * rr + 1]);
     // byte offsets of the staged pieces (vrow, k-block kb) of bf16(-S): all k-blocks (MM1
     // operands), and this wave's own ones (where it stages its rows)
     int soff[KB], sown[KBH];
@@ -644,10 +678,14 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
       for (int ib = 0; ib < KBH; ++ib) {
         u32x4 w;
-        w[0] = pack_bf16x2(-S[2 * ib][0], -S[2 * ib][1]);
-        w[1] = pack_bf16x2(-S[2 * ib][2], -S[2 * ib][3]);
-        w[2] = pack_bf16x2(-S[2 * ib + 1][0], -S[2 * ib + 1][1]);
-        w[3] = pack_bf16x2(-S[2 * ib + 1][2], -S[2 * ib + 1][3]);
+        if constexpr (NUM == 1) {
+          w = u32x4{Sp[2 * ib][0], Sp[2 * ib][1], Sp[2 * ib + 1][0], Sp[2 * ib + 1][1]} ^ 0x80008000u;
+        } else {
+          w[0] = pack_bf16x2(-S[2 * ib][0], -S[2 * ib][1]);
+          w[1] = pack_bf16x2(-S[2 * ib][2], -S[2 * ib][3]);
+          w[2] = pack_bf16x2(-S[2 * ib + 1][0], -S[2 * ib + 1][1]);
+          w[3] = pack_bf16x2(-S[2 * ib + 1][2], -S[2 * ib + 1][3]);
+        }
         *(u32x4*)(ss + sown[ib]) = w;
       }
     };
@@ -714,7 +752,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       };
       u32x4 kop0[KTH], kop1[KTH];
-      unsigned hdp[CONTEST ? KTH : 1][2];
+      unsigned hdp[FULL ? KTH : 1][2];
+      float hdf[NUM == 1 ? KTH : 1][4];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -730,8 +769,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         } else if constexpr (CONTEST) {
           const h16x2 a16 = to_h16x2(a, a);
 #pragma unroll
-          for (int rr = 0; rr < 2; ++rr)
-            hdp[i][rr] = opaque(h16x2_to_bf16x2(to_h16x2(S[i][2 * rr], S[i][2 * rr + 1]) * a16));
+          for (int rr = 0; rr < 2; ++rr) contest_decay_pair(Sp[i][rr], a16, hdf[i][2 * rr], hdf[i][2 * rr + 1]);
           S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[i] = S[i] * a;
@@ -818,11 +856,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             }
           } else {
 #pragma unroll
-            for (int rr = 0; rr < 2; ++rr) {
-              const unsigned sw = contest_combine_pair(S[i][2 * rr], S[i][2 * rr + 1], hdp[i][rr]);
-              S[i][2 * rr] = bf16_lo(sw);
-              S[i][2 * rr + 1] = bf16_hi(sw);
-            }
+            for (int rr = 0; rr < 2; ++rr)
+              Sp[i][rr] = contest_combine_pair(S[i][2 * rr], S[i][2 * rr + 1], hdf[i][2 * rr], hdf[i][2 * rr + 1]);
           }
         }
       }
@@ -840,6 +875,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
 
     if constexpr (NUM == 1) {
+#pragma unroll
+      for (int i = 0; i < KTH; ++i)
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          S[i][2 * rr] = bf16_lo(Sp[i][rr]);
+          S[i][2 * rr + 1] = bf16_hi(Sp[i][rr]);
+        }
       bool bad = false;
 #pragma unroll
       for (int i = 0; i < KTH; ++i)
@@ -883,6 +925,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // contest fast pass: the bf16 state kept as packed pairs between chunks
+    unsigned Sp[NUM == 1 ? KT : 1][2];
+    if constexpr (NUM == 1)
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) Sp[kt][r] = pack_bf16x2(S[kt][2 * r], S[kt][2 * r + 1]);
     block_barrier();   // P: stage 0 ready
 
     // One chunk; the stage (c % STAGES) and the staging buffer (c % 2) are template constants,
@@ -928,10 +977,14 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       u32x4 Sw[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        Sw[kb][0] = pack_bf16x2(-S[2 * kb][0], -S[2 * kb][1]);
-        Sw[kb][1] = pack_bf16x2(-S[2 * kb][2], -S[2 * kb][3]);
-        Sw[kb][2] = pack_bf16x2(-S[2 * kb + 1][0], -S[2 * kb + 1][1]);
-        Sw[kb][3] = pack_bf16x2(-S[2 * kb + 1][2], -S[2 * kb + 1][3]);
+        if constexpr (NUM == 1) {
+          Sw[kb] = u32x4{Sp[2 * kb][0], Sp[2 * kb][1], Sp[2 * kb + 1][0], Sp[2 * kb + 1][1]} ^ 0x80008000u;
+        } else {
+          Sw[kb][0] = pack_bf16x2(-S[2 * kb][0], -S[2 * kb][1]);
+          Sw[kb][1] = pack_bf16x2(-S[2 * kb][2], -S[2 * kb][3]);
+          Sw[kb][2] = pack_bf16x2(-S[2 * kb + 1][0], -S[2 * kb + 1][1]);
+          Sw[kb][3] = pack_bf16x2(-S[2 * kb + 1][2], -S[2 * kb + 1][3]);
+        }
       }
       {
         u32x4* ss = (u32x4*)(smem + L::SS_OFF + par * L::SS_BYTES);
@@ -966,7 +1019,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         }
       };
       u32x4 kop0[KT], kop1[KT];
-      unsigned hdp[CONTEST ? KT : 1][2];   // contest: bf16(hd) pairs of the decayed state
+      unsigned hdp[FULL ? KT : 1][2];      // contest, full pass: bf16(hd) pairs of the decayed state
+      float hdf[NUM == 1 ? KT : 1][4];     // contest, fast pass: bf16(hd) as floats
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -985,8 +1039,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           // packed fp16 products of fp16(S) and the fp16 decay a
           const h16x2 a16 = to_h16x2(a, a);
 #pragma unroll
-          for (int r = 0; r < 2; ++r)
-            hdp[kt][r] = opaque(h16x2_to_bf16x2(to_h16x2(S[kt][2 * r], S[kt][2 * r + 1]) * a16));
+          for (int r = 0; r < 2; ++r) contest_decay_pair(Sp[kt][r], a16, hdf[kt][2 * r], hdf[kt][2 * r + 1]);
           S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
           S[kt] = S[kt] * a;
@@ -1071,11 +1124,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             }
           } else {
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              const unsigned sw = contest_combine_pair(S[kt][2 * r], S[kt][2 * r + 1], hdp[kt][r]);
-              S[kt][2 * r] = bf16_lo(sw);
-              S[kt][2 * r + 1] = bf16_hi(sw);
-            }
+            for (int r = 0; r < 2; ++r)
+              Sp[kt][r] = contest_combine_pair(S[kt][2 * r], S[kt][2 * r + 1], hdf[kt][2 * r], hdf[kt][2 * r + 1]);
           }
         }
       }
@@ -1092,6 +1142,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
 
     if constexpr (NUM == 1) {
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          S[kt][2 * r] = bf16_lo(Sp[kt][r]);
+          S[kt][2 * r + 1] = bf16_hi(Sp[kt][r]);
+        }
       bool bad = false;
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt)
@@ -1388,7 +1445,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     }
     if (touching) wait_vm<0>();   // the touches write this workgroup's LDS: drain them
     if constexpr (NUM == 1)
-      if (__any((amax & 0xffffu) > 0x477fu || (amax >> 16) > 0x477fu) && lane == 0)
+      if (__any((amax & 0x7fffu) > 0x477fu || ((amax >> 16) & 0x7fffu) > 0x477fu) && lane == 0)
         p.redo[(int64_t)tk.n * p.H + tk.head] = p.epoch;
   } else if (wave == NCWT + L::NSW + NLW) {
     // ------------------------------------------------------------------ gate wave

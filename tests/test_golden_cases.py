@@ -308,6 +308,34 @@ def test_contest_kernel_padded_head_dims(dev, D):
 
 
 @pytest.mark.gpu
+def test_contest_kernel_subnormal_updates(dev):
+    """u of order 1e-5: v16, the gated vd and the state updates K^T vd sit in fp16's subnormal
+    range (below 6.1e-5), where the fast pass's mixed fp16/fp32 additions and conversions must
+    keep every bit; against the O2 oracle, with a decaying gate, grouped heads and an initial
+    state of the same order."""
+    print("[contest] subnormal updates", flush=True)
+    rng = np.random.default_rng(21)
+    T, HV, HK, D = 300, 4, 2, 128
+    k = O.bf16_round((rng.random((1, T, HK, D)) * 2 - 1).astype(np.float32))
+    w = O.bf16_round(((rng.random((1, HV, T, D)) * 2 - 1) / D).astype(np.float32))
+    u = O.bf16_round(((rng.random((1, HV, T, D)) * 2 - 1) * 2e-5).astype(np.float32))
+    h0 = O.bf16_round((rng.standard_normal((2, HV, D, D)) * 1e-5).astype(np.float32))
+    cu = np.array([0, 180, 300], np.int64)
+    g = np.zeros((1, HV, T), np.float32)
+    for i0, i1 in ((0, 64), (64, 128), (128, 180), (180, 244), (244, 300)):
+        g[..., i0:i1] = -0.02 * np.arange(1, i1 - i0 + 1, dtype=np.float32)
+    a = dict(input_k=k, input_w=w, input_u=u, input_g=g, input_initial_state=h0, input_cu_seqlens=cu)
+    got = _run_contest(dev, a)
+    ref = O.fwd_h_o2(k, w, u, g, h0, cu)
+    sub = (np.abs(ref[1]) > 0) & (np.abs(ref[1]) < 6.1e-5)
+    assert sub.mean() > 0.5, sub.mean()             # most v_new values are fp16 subnormals
+    for name, x, r in zip(("h", "v", "final"), got, ref):
+        exact = (x == r).mean()
+        assert exact >= O2_MIN_EXACT, (name, exact)
+        assert np.abs(x - r).max() <= 1e-2 * np.abs(r).max(), name
+
+
+@pytest.mark.gpu
 def test_contest_kernel_without_v_new_output(dev):
     """Token-major calls, u beyond the fp16 range on one head: that shows first in the staged
     v_new, which the fast pass checks whether or not v_new is an output.  With v_new requested
