@@ -626,7 +626,8 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
     // state rows of MM2 tiles kt = KT/2 r .. KT/2 r + KT/2 - 1 (k = KD/2 r .. KD/2 r + KD/2 - 1).
     // MM1 for token block tb = r takes the whole bf16(-S) of its columns, its own rows and its
     // partner's, from the staging buffer the store waves read for the h snapshot (three buffers:
-    // bf16(-S) of chunk c+1 is staged at the end of chunk c).  MM2 of its rows needs Vd of both
+    // bf16(-S) of chunk c+1 is staged at the end of chunk c; the contest fast pass stages +S, as
+    // its MM1 starts from zero and the epilogue subtracts).  MM2 of its rows needs Vd of both
     // token blocks, so the two partners swap Vd through LDS once per chunk (1 KiB each, with a
     // flag).  Each wave reads half of the W and K^T operands and does half of the MFMA and VALU
     // work of a wave that owns all rows; every accumulation chain runs in the same order
@@ -686,7 +687,7 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
       for (int ib = 0; ib < KBH; ++ib) {
         u32x4 w;
         if constexpr (NUM == 1) {
-          w = u32x4{Sp[2 * ib][0], Sp[2 * ib][1], Sp[2 * ib + 1][0], Sp[2 * ib + 1][1]} ^ 0x80008000u;
+          w = u32x4{Sp[2 * ib][0], Sp[2 * ib][1], Sp[2 * ib + 1][0], Sp[2 * ib + 1][1]};   // +S
         } else {
           w[0] = pack_bf16x2(-S[2 * ib][0], -S[2 * ib][1]);
           w[1] = pack_bf16x2(-S[2 * ib][2], -S[2 * ib][3]);
@@ -816,8 +817,10 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
             pv[jj] = pack_bf16x2(x0, x1);
             pd[jj] = pack_bf16x2(f16_sat(x0 * gm[hh][rr]), f16_sat(x1 * gm[hh][rr + 1]));
           } else {
-            const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(v0, v1));
-            pv[jj] = h16x2_to_bf16x2(x16);
+            // acc = +W S (the fast pass stages +S): v16 = fp16(u) + fp16(bf16(-acc)); v16 is
+            // staged as fp16
+            const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(-v0, -v1));
+            pv[jj] = __builtin_bit_cast(unsigned, x16);
             pd[jj] = h16x2_to_bf16x2(x16 * as_h16x2(g16[jj]));
           }
         } else {
@@ -988,12 +991,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         for (int kb = 0; kb < KB; ++kb) wop[tt][kb] = wrow[(4 * kb + g) ^ swz_w<P>(row)];
       }
       // bf16(-S): the MM1 B operands (so MM1 accumulates U - W S onto U) and the h snapshot,
-      // staged sign-flipped (the store wave flips it back).
+      // staged sign-flipped (the store wave flips it back).  The contest fast pass uses +S: its
+      // MM1 starts from zero and the epilogue subtracts, so nothing is flipped there.
       u32x4 Sw[KB];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         if constexpr (NUM == 1) {
-          Sw[kb] = u32x4{Sp[2 * kb][0], Sp[2 * kb][1], Sp[2 * kb + 1][0], Sp[2 * kb + 1][1]} ^ 0x80008000u;
+          Sw[kb] = u32x4{Sp[2 * kb][0], Sp[2 * kb][1], Sp[2 * kb + 1][0], Sp[2 * kb + 1][1]};   // +S
         } else {
           Sw[kb][0] = pack_bf16x2(-S[2 * kb][0], -S[2 * kb][1]);
           Sw[kb][1] = pack_bf16x2(-S[2 * kb][2], -S[2 * kb][3]);
@@ -1092,9 +1096,11 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
               pv[j] = pack_bf16x2(x0, x1);
               pd[j] = pack_bf16x2(f16_sat(x0 * gm[tb][hh][r]), f16_sat(x1 * gm[tb][hh][r + 1]));
             } else {
-              // v16 = fp16(u) - fp16(bf16(W S)) = fp16(u) + fp16(bf16(acc)), acc = -W S
-              const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(v0, v1));
-              pv[j] = h16x2_to_bf16x2(x16);
+              // v16 = fp16(u) - fp16(bf16(W S)) = fp16(u) + fp16(bf16(-acc)), acc = +W S (the fast
+              // pass stages +S; the negation is a source modifier of the bf16 conversion); v16 is
+              // staged as fp16 and rounded to bf16 by the store waves
+              const h16x2 x16 = to_h16x2(u0, u1) + bf16x2_to_h16x2(pack_bf16x2(-v0, -v1));
+              pv[j] = __builtin_bit_cast(unsigned, x16);
               pd[j] = h16x2_to_bf16x2(x16 * as_h16x2(g16[tb][j]));
             }
           } else {
@@ -1402,8 +1408,9 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
         u32x4 hv;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-          hv[2 * half] = hx[m][half][0] ^ 0x80008000u;       // staged as bf16(-S)
-          hv[2 * half + 1] = hx[m][half][1] ^ 0x80008000u;
+          // staged as bf16(-S), or as bf16(+S) by the contest fast pass
+          hv[2 * half] = NUM == 1 ? hx[m][half][0] : hx[m][half][0] ^ 0x80008000u;
+          hv[2 * half + 1] = NUM == 1 ? hx[m][half][1] : hx[m][half][1] ^ 0x80008000u;
           if constexpr (NUM == 1) amax = pk_absmax_bf16(pk_absmax_bf16(amax, hx[m][half][0]), hx[m][half][1]);
         }
         if (k0 < p.K) *(u32x4*)(hdst + (int64_t)(k0 + i) * p.V + v0) = hv;   // rows >= K: padding
@@ -1415,7 +1422,13 @@ cgdr_fwd_h_bf16_kernel(const FwdHParams p) {
           if ((MH + m) % L::NSW != SW) continue;
           const int unit = 4 * m + blk;
           const int t0 = 16 * (unit / (VT / 8)), v0 = 8 * (unit % (VT / 8));
-          const u32x4 vv = {vx[m][0][0], vx[m][0][1], vx[m][1][0], vx[m][1][1]};
+          u32x4 vv = {vx[m][0][0], vx[m][0][1], vx[m][1][0], vx[m][1][1]};
+          if constexpr (NUM == 1) {
+            // the fast pass stages v16 as fp16 pairs: v_new = bf16(v16)
+            const unsigned w0 = vx[m][0][0], w1 = vx[m][0][1], w2 = vx[m][1][0], w3 = vx[m][1][1];
+            vv = u32x4{h16x2_to_bf16x2(as_h16x2(w0)), h16x2_to_bf16x2(as_h16x2(w1)),
+                       h16x2_to_bf16x2(as_h16x2(w2)), h16x2_to_bf16x2(as_h16x2(w3))};
+          }
           if (t0 + i < len) {
             if (vbase_ptr != nullptr) *(u32x4*)(vdst + (int64_t)(t0 + i) * p.sv_t + v0) = vv;
             if constexpr (NUM == 1)
