@@ -20,7 +20,7 @@ from __future__ import annotations
 import torch
 
 from . import _abi
-from .fwd_h import CHUNK_SIZE, _prep_input, _ptr, _varlen_meta
+from .fwd_h import CHUNK_SIZE, _host_to_device, _prep_input, _ptr, _varlen_meta
 
 
 def _args(q, k, v, h, g, cu_dev, ci_dev, o, scale, N, NT) -> _abi.ChunkOArgs:
@@ -78,10 +78,10 @@ def chunk_fwd_o(
     else:
         if B != 1:
             raise ValueError(f"cu_seqlens requires B == 1, got B={B}")
-        N, NT, cu_dev, _ = _varlen_meta(cu_seqlens, T, chunk_indices, None, dev)
-        ci_dev = torch.tensor(_abi.prepare_chunk_indices(
+        N, NT, cu_dev, _ = _varlen_meta(cu_seqlens, T, chunk_indices, None, dev, want_offsets=False)
+        ci_dev = _host_to_device(_abi.prepare_chunk_indices(
             [int(x) for x in cu_seqlens.detach().to("cpu", torch.int64).tolist()], CHUNK_SIZE),
-            dtype=torch.int64, device=dev).reshape(-1, 2) if NT > 0 else None
+            dev).reshape(-1, 2) if NT > 0 else None
     if tuple(h.shape) != (B, NT, H, K, V):
         raise ValueError(f"h must have shape [B,NT,H,K,V]={[B, NT, H, K, V]}, got {list(h.shape)}")
     if g is not None:

@@ -55,10 +55,23 @@ def _prep_input(t: torch.Tensor, name: str, align: int) -> torch.Tensor:
     return t
 
 
-def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets, device):
+def _host_to_device(vals, device) -> torch.Tensor:
+    """int64 values from the host to the device through pinned memory, without blocking the host:
+    a copy from pageable memory would wait for the stream's earlier work, leaving the GPU idle
+    while the host prepares the next call.  (torch keeps the pinned block until the copy is done.)"""
+    host = torch.as_tensor(vals, dtype=torch.int64)
+    if device.type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
+
+
+def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets, device,
+                 want_offsets: bool = True):
     """Host validation of cu_seqlens (``code/tests/golden/generate_golden.py:326-339``,
     ``code/op_host/chunk_gated_delta_rule_fwd_h_infershape.cpp:240-275``) and the device
-    chunk offsets.  Returns (N, NT, cu_device_int64, chunk_offsets_device_int64)."""
+    chunk offsets.  Returns (N, NT, cu_device_int64, chunk_offsets_device_int64 or None).
+    A cu_seqlens on the host is read without a device round trip; one on the device is copied
+    to the host once (NT, the leading dimension of h, depends on it)."""
     if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
         raise ValueError("cu_seqlens must be one-dimensional with at least two entries")
     cu_host = [int(x) for x in cu_seqlens.detach().to("cpu", torch.int64).tolist()]
@@ -79,8 +92,11 @@ def _varlen_meta(cu_seqlens: torch.Tensor, T: int, chunk_indices, chunk_offsets,
         co = [int(x) for x in chunk_offsets.detach().to("cpu", torch.int64).tolist()]
         if co[: N + 1] != offs:
             raise ValueError("chunk_offsets does not match cu_seqlens")
-    cu_dev = cu_seqlens.to(device=device, dtype=torch.int64).contiguous()
-    offs_dev = torch.tensor(offs, dtype=torch.int64, device=device)
+    if cu_seqlens.device == device and cu_seqlens.dtype == torch.int64 and cu_seqlens.is_contiguous():
+        cu_dev = cu_seqlens
+    else:
+        cu_dev = _host_to_device(cu_host, device)
+    offs_dev = _host_to_device(offs, device) if want_offsets else None
     return N, NT, cu_dev, offs_dev
 
 

@@ -64,7 +64,7 @@ def wy_fwd(
     else:
         if B != 1:
             raise ValueError(f"cu_seqlens requires B == 1, got B={B}")
-        N, NT, cu_dev, _ = _varlen_meta(cu_seqlens, T, chunk_indices, None, dev)
+        N, NT, cu_dev, _ = _varlen_meta(cu_seqlens, T, chunk_indices, None, dev, want_offsets=False)
         ci_dev = None
     k, v = _prep_input(k, "k", 16), _prep_input(v, "v", 16)
     w = torch.empty(B, T, H, K, dtype=torch.bfloat16, device=dev)
