@@ -220,6 +220,10 @@ def test_chunk_o_kernel_matches_oracle(dev, B, T, H, Hg, K, V, gate, shift, cu):
     o = cgdr_amd.chunk_fwd_o(q, k, v, h, g=g, scale=0.5, cu_seqlens=cud)
     torch.cuda.synchronize()
     _check(o, inp, 0.5)
+    if cud is not None:   # cu_seqlens on the host (copied through pinned memory): the same bits
+        o2 = cgdr_amd.chunk_fwd_o(q, k, v, h, g=g, scale=0.5, cu_seqlens=cud.cpu())
+        torch.cuda.synchronize()
+        assert torch.equal(o, o2)
 
 
 def _abi_o(q, k, v, h, g, cu, ci, o, scale, N, NT):

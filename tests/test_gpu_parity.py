@@ -422,6 +422,14 @@ def test_python_wrapper_varlen_and_chunk_indices(dev):
     torch.cuda.synchronize()
     for x, y in zip(ref, (h, v, f)):
         assert torch.equal(x, y)
+    # cu_seqlens on the host (int64 and int32): copied to the device through pinned memory
+    for cu_host in (torch.from_numpy(cu), torch.from_numpy(cu.astype(np.int32))):
+        out = cgdr_amd.chunk_gated_delta_rule_fwd_h(d["k"], d["w"], d["u"], g=d["g"],
+                                                    initial_state=d["initial_state"], output_final_state=True,
+                                                    cu_seqlens=cu_host)
+        torch.cuda.synchronize()
+        for x, y in zip(ref, out):
+            assert torch.equal(x, y)
     with pytest.raises(ValueError):
         cgdr_amd.chunk_gated_delta_rule_fwd_h(d["k"], d["w"], d["u"], g=d["g"], cu_seqlens=d["cu_seqlens"],
                                               chunk_indices=ci[:-1])
