@@ -407,6 +407,39 @@ def test_contest_kernel_rising_gates_and_large_state(dev):
 
 
 @pytest.mark.gpu
+def test_contest_kernel_full_length(dev):
+    """Contest numerics over the headline's sequence length, T = 32768 (512 chunks), on four
+    heads, with the headline's plan (32-column tiles, helper workgroups, two compute waves per 16
+    columns), against the O2 oracle.  The first 64 chunks are held to the golden cases' bit-exact
+    share.  Further on, the two bf16 GEMMs of a chunk accumulate in a different order on the MFMAs
+    than in the oracle's (or the reference's) CPU GEMM, the resulting 1-ulp differences pass
+    through the bf16 state, and the exact share falls slowly (measured on MI355X: h 100 % at chunk
+    8, 99.2 % at 64, 95.6 % at 511); the deviation stays bounded: every element within 1 % of the
+    tensor's largest magnitude, and at least 95 % of them bit-exact."""
+    print("[contest] T=32768 H=4", flush=True)
+    inp = O.make_inputs(81, 1, 32768, 4, 128, 128, gate="linear", with_h0=True, profile="golden")
+    h0 = O.bf16_round(inp["initial_state"])
+    w = np.swapaxes(inp["w"], 1, 2).copy()
+    u = np.swapaxes(inp["u"], 1, 2).copy()
+    g = np.swapaxes(inp["g"], 1, 2).copy()
+    cu = np.array([0, 32768], np.int64)
+    a = dict(input_k=inp["k"], input_w=w, input_u=u, input_g=g, input_cu_seqlens=cu, input_initial_state=h0)
+    got = _run_contest(dev, a)
+    ref = O.fwd_h_o2(inp["k"], w, u, g, h0, cu)
+    early = (got[0][0, :, :64] == ref[0][0, :, :64]).mean()
+    print(f"  h, first 64 chunks: bit-exact {early:.5f}", flush=True)
+    assert early >= O2_MIN_EXACT, early
+    assert (got[1][0, :, :4096] == ref[1][0, :, :4096]).mean() >= O2_MIN_EXACT
+    for name, x, r in zip(("h", "v", "final"), got, ref):
+        same = (x == r).mean()
+        err = np.abs(x - r).max() / np.abs(r).max()
+        print(f"  {name}: bit-exact {same:.5f}, max |err| / max |ref| {err:.3e}", flush=True)
+        assert np.isfinite(x).all(), name
+        assert same >= 0.95, (name, same)
+        assert err <= 0.01, (name, err)
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("case", [c for c in CASES if c.name in ("long_1024_single", "grouped_heads_packed")],
                          ids=lambda c: c.name)
 def test_runner_contest_mode(dev, case, tmp_path):
