@@ -33,6 +33,7 @@ sys.path.insert(0, os.path.join(ROOT, "cann-operator-challenge-august_amd"))
 METRIC = "tokens/sec + achieved HBM GB/s at B=1,T=32k,H=32,K=V=128 bf16 (1 GPU)"
 HBM_PEAK_GBPS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+F32_MFMA_PEAK_TFLOPS = 157.3   # dense fp32 MFMA, MI355X
 WORKLOAD = dict(B=1, T=32768, H=32, Hg=32, K=128, V=128, chunk_size=64)
 
 
@@ -530,7 +531,7 @@ def main():
         "kernel_ms": avg_ms,
         "kernel_ms_min": min(kern_ms),
         "tflops": flops / (avg_ms * 1e-3) / 1e12,
-        "mfma_util": flops / (avg_ms * 1e-3) / 1e12 / BF16_MFMA_PEAK_TFLOPS,
+        "mfma_util": flops / (avg_ms * 1e-3) / 1e12 / (F32_MFMA_PEAK_TFLOPS if es == 4 else BF16_MFMA_PEAK_TFLOPS),
         "plan": plan,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,

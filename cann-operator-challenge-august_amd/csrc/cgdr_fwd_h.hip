@@ -145,7 +145,8 @@ cgdr_status check_tuning(const cgdr_fwd_h_tuning* tu) {
   if (tu->helper_lead < -1) return fail(CGDR_ERR_INVALID, "tuning.helper_lead must be >= -1");
   if (tu->helper_waves < 0 || tu->helper_waves > 16) return fail(CGDR_ERR_INVALID, "tuning.helper_waves must be in [0, 16]");
   if (tu->cu_count < 0 || tu->xcd_count < 0) return fail(CGDR_ERR_INVALID, "tuning.cu_count/xcd_count must be >= 0");
-  if (tu->row_split < 0 || tu->row_split > 2) return fail(CGDR_ERR_INVALID, "tuning.row_split must be 0, 1 or 2");
+  if (tu->row_split < 0 || tu->row_split > 4 || tu->row_split == 3)
+    return fail(CGDR_ERR_INVALID, "tuning.row_split must be 0, 1, 2 or 4");
   return CGDR_OK;
 }
 
@@ -212,6 +213,24 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     ncw = forced / 16;
   } else if (use_helpers) {
     ncw = 2;
+  } else if (a->in_dtype == CGDR_F32) {
+    // fp32: all four waves of a task compute at every tile width (the row split, K up to 128;
+    // at K = 256 the waves of one tile's 16-column blocks), so a task's time per chunk grows with
+    // its width while wider tiles read W and K fewer times.  Pick the width with the least
+    // (rounds of the device) x (time of one round relative to 16 columns), the latter measured
+    // with one task per CU: K = 128, 32 chunks: 109 / 177 / 245 us at 16 / 32 / 64 columns;
+    // K = 256: 587 / 665 / 716 us.  At B=4, T=4096, H=32, K=V=128 (1,024 / 512 / 256 tasks, 4 / 2
+    // / 1 rounds) this picks 64 columns: 581 us against 906 / 786 us at 16 / 32 columns.
+    static const double cost_rs[3] = {1.0, 1.62, 2.25}, cost_256[3] = {1.0, 1.13, 1.22};
+    const double* cost = kd <= 128 ? cost_rs : cost_256;
+    ncw = 1;
+    double best = 0.0;
+    for (int i = 0, w = 1; w <= 4; ++i, w *= 2) {
+      if (V % (16 * w) != 0) break;
+      const int64_t tasks = pairs * (V / (16 * w));
+      const double t = (double)((tasks + cus - 1) / cus) * cost[i];
+      if (w == 1 || t < best) best = t, ncw = w;
+    }
   } else {
     // Enough workgroups to cover the CUs first, then wider V-tiles (fewer K/W re-reads).
     ncw = 1;
@@ -230,6 +249,15 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     pl->nlw = 0;
     pl->stages = 1;
     pl->threads = cgdr::F32Layout<32, 1>::THREADS;   // four waves at every key dim
+    // Row split: all four waves compute (wave (j, r) holds state rows KD/RSF r .. of column block
+    // j), where the staging buffers fit (K up to 128) and each wave keeps whole 16-row tiles.
+    int rs = tu != nullptr ? tu->row_split : 0;
+    const int kt = kd / 16;
+    const int full = 4 / ncw;                      // 4, 2 or 1 row groups per column block
+    int best = (kd <= 128) ? (kt % full == 0 ? full : (kt % 2 == 0 && full >= 2 ? 2 : 1)) : 1;
+    if (rs == 0 || rs > best || (rs != 1 && rs != 2 && rs != 4)) rs = best;
+    if (rs > 1 && kt % rs != 0) rs = 1;
+    pl->rs = rs;
   } else {
     // bf16: the pipelined kernel, with the contest rounding model when asked for
     pl->kernel = a->numerics == CGDR_NUMERICS_CONTEST ? 2 : 0;
@@ -250,6 +278,7 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     // an even number of 32-row state blocks (K of 64 or 128 here) and at most 8 waves.
     int rs = tu != nullptr ? tu->row_split : 0;
     if (rs == 0) rs = pl->kernel == 2 ? 2 : 1;
+    if (rs == 4) rs = 2;   // the bf16 kernels split the rows two ways at most
     if (rs == 2 && !(kd == 64 || kd == 128) ) rs = 1;
     if (rs == 2 && ncw > 2) rs = 1;
     while (nlw > 1 && (rs + 1) * ncw + nlw + 1 > 8) nlw /= 2;
@@ -369,8 +398,14 @@ int lds_bytes_of(const Plan& pl, int64_t K) {
   if (pl.kernel == 1) {
     auto f32 = [&](auto kd) -> int {
       constexpr int KD = decltype(kd)::value;
-      return pl.ncw == 1 ? cgdr::F32Layout<KD, 1>::LDS_BYTES
-                         : pl.ncw == 2 ? cgdr::F32Layout<KD, 2>::LDS_BYTES : cgdr::F32Layout<KD, 4>::LDS_BYTES;
+      auto by_rs = [&](auto c) -> int {
+        constexpr int NCW = decltype(c)::value;
+        if (pl.rs == 4) return cgdr::F32Layout<KD, NCW, 4>::LDS_BYTES;
+        if (pl.rs == 2) return cgdr::F32Layout<KD, NCW, 2>::LDS_BYTES;
+        return cgdr::F32Layout<KD, NCW, 1>::LDS_BYTES;
+      };
+      return pl.ncw == 1 ? by_rs(std::integral_constant<int, 1>{})
+                         : pl.ncw == 2 ? by_rs(std::integral_constant<int, 2>{}) : by_rs(std::integral_constant<int, 4>{});
     };
     switch (kernel_kd(K)) {
       case 32: return f32(std::integral_constant<int, 32>{});

@@ -17,7 +17,7 @@ struct Plan {
   int kernel;        // 0 bf16 pipeline, 1 fp32, 2 bf16 with the contest numerics (two passes)
   int helpers;       // bf16: one L2-prefetch workgroup per task
   int ncw;           // 16-column blocks (Vt = 16 * ncw)
-  int rs;            // bf16 pipeline: compute waves per 16-column block (2: state rows split)
+  int rs;            // compute waves per 16-column block (bf16: 2 = state rows split; fp32: 1, 2, 4)
   int nlw;           // load waves (bf16 pipeline)
   int stages;        // LDS ring depth (bf16 pipeline)
   int threads;
@@ -35,11 +35,22 @@ hipError_t launch_bf16(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t str
   return hipGetLastError();
 }
 
-template <int KD, int NCW>
+template <int KD, int NCW, int RSF = 1>
 hipError_t launch_f32(const cgdr::FwdHParams& p, int64_t tasks, hipStream_t stream) {
-  using L = cgdr::F32Layout<KD, NCW>;
-  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream, p);
+  using L = cgdr::F32Layout<KD, NCW, RSF>;
+  hipLaunchKernelGGL((cgdr::cgdr_fwd_h_f32_kernel<KD, NCW, RSF>), dim3((unsigned)tasks), dim3(L::THREADS), 0, stream,
+                     p);
   return hipGetLastError();
+}
+
+// fp32: the row split RSF the plan picked (instantiated where it fits, see f32_config_ok)
+template <int KD, int NCW>
+hipError_t dispatch_f32(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
+  if constexpr (cgdr::f32_config_ok<KD, NCW, 4>())
+    if (pl.rs == 4) return launch_f32<KD, NCW, 4>(p, pl.tasks, s);
+  if constexpr (cgdr::f32_config_ok<KD, NCW, 2>())
+    if (pl.rs == 2) return launch_f32<KD, NCW, 2>(p, pl.tasks, s);
+  return launch_f32<KD, NCW, 1>(p, pl.tasks, s);
 }
 
 // NUM: the kernel's numerics mode (0 default, 1 contest fast pass, 2 contest full pass).
@@ -100,9 +111,9 @@ template <int KD>
 hipError_t launch_kd(const cgdr::FwdHParams& p, const Plan& pl, hipStream_t s) {
   if (pl.kernel == 0) return dispatch_bf16<KD, 0>(p, pl, s);
   if (pl.kernel == 2) return dispatch_contest<KD>(p, pl, s);
-  if (pl.ncw == 2) return launch_f32<KD, 2>(p, pl.tasks, s);
-  if (pl.ncw == 4) return launch_f32<KD, 4>(p, pl.tasks, s);
-  return launch_f32<KD, 1>(p, pl.tasks, s);
+  if (pl.ncw == 2) return dispatch_f32<KD, 2>(p, pl, s);
+  if (pl.ncw == 4) return dispatch_f32<KD, 4>(p, pl, s);
+  return dispatch_f32<KD, 1>(p, pl, s);
 }
 
 extern template hipError_t launch_kd<32>(const cgdr::FwdHParams&, const Plan&, hipStream_t);

@@ -1531,13 +1531,19 @@ cgdr_g_head_major_kernel(const float* __restrict__ g, float* __restrict__ gt, in
 // =============================================================================================
 // fp32 kernel (fp32 k/w/u/h/v_new): same task decomposition and the same tile orderings
 // (pi, sigma) with v_mfma_f32_16x16x4_f32, whose operands are one element per lane, so no
-// transposed reads are needed.  Four waves per workgroup: waves 0 .. NCW-1 compute; all four
-// load chunk c+1 into registers (16-byte loads) while chunk c is computed, and store it to LDS
-// after the chunk's barrier.  It is the exact-arithmetic path (fp32 products, fp32
-// accumulation).
+// transposed reads are needed.  Four waves per workgroup; all four load chunk c+1 into
+// registers (16-byte loads) while chunk c is computed, and store it to LDS after the chunk's
+// barrier.  It is the exact-arithmetic path (fp32 products, fp32 accumulation).
+// RSF = 1: waves 0 .. NCW-1 compute, one per 16 value columns.  RSF > 1 (NCW * RSF <= 4): wave
+// (j, r) = (wave % NCW, wave / NCW) holds state rows KD/RSF r .. KD/RSF (r+1) - 1 of column
+// block j and runs MM1 for token tiles 4/RSF r .. 4/RSF (r+1) - 1; the full state of a column
+// block reaches MM1 through an fp32 staging buffer, and Vd of all 64 tokens reaches MM2 through
+// another, with one more barrier per chunk.  Every accumulation chain keeps its order (MM1:
+// k-blocks in order; MM2: a S, then token tiles in order), so the results are the RSF = 1
+// results bit for bit.
 // =============================================================================================
 
-template <int KD, int NCW>
+template <int KD, int NCW, int RSF = 1>
 struct F32Layout {
   static constexpr int VT = 16 * NCW;
   static constexpr int WP = KD + 4;     // padded row pitch (floats)
@@ -1545,32 +1551,60 @@ struct F32Layout {
   static constexpr int K_OFF = 64 * WP * 4;
   static constexpr int U_OFF = 2 * 64 * WP * 4;
   static constexpr int G_OFF = U_OFF + 64 * (VT + 4) * 4;
-  static constexpr int LDS_BYTES = G_OFF + 80 * 4;
+  static constexpr int SSP = KD + 4;    // row split: state staging [VT columns][KD], padded
+  static constexpr int SS_OFF = G_OFF + 80 * 4;
+  static constexpr int SS_BYTES = RSF > 1 ? VT * SSP * 4 : 0;
+  static constexpr int VDP = 64 + 4;    // row split: Vd staging [VT columns][64 tokens], padded
+  static constexpr int VD_OFF = SS_OFF + SS_BYTES;
+  static constexpr int VD_BYTES = RSF > 1 ? VT * VDP * 4 : 0;
+  static constexpr int LDS_BYTES = VD_OFF + VD_BYTES;
   static constexpr int THREADS = 256;                 // four waves load; NCW of them compute
   static constexpr int PW = 64 * KD / 4 / THREADS;    // 16-byte pieces per thread of the W (and K) tile
   static constexpr int PU = 64 * VT / 4 / THREADS;    // ... of the U tile
 };
 
-template <int KD, int NCW>
+// The fp32 row split needs whole 16-row state tiles per wave and at most four compute waves,
+// and its staging buffers must fit beside the tiles (K up to 128).
+template <int KD, int NCW, int RSF>
+constexpr bool f32_config_ok() {
+  return RSF == 1 || (NCW * RSF <= 4 && (KD / 16) % RSF == 0 && KD <= 128 &&
+                      F32Layout<KD, NCW, RSF>::LDS_BYTES <= 160 * 1024);
+}
+
+template <int KD, int NCW, int RSF = 1>
 __global__ void __launch_bounds__(256)
 cgdr_fwd_h_f32_kernel(const FwdHParams p) {
-  using L = F32Layout<KD, NCW>;
+  using L = F32Layout<KD, NCW, RSF>;
+  static_assert(f32_config_ok<KD, NCW, RSF>(), "fp32 row split configuration");
   constexpr int VT = L::VT, WP = L::WP, UP = VT + 4;
   constexpr int KT = KD / 16;
+  constexpr int KTR = KT / RSF;         // own state tiles
+  constexpr int TPW = 4 / RSF;          // own MM1 token tiles (RSF > 1)
+  constexpr int SSP = L::SSP, VDP = L::VDP;
   __shared__ __attribute__((aligned(16))) float smem[L::LDS_BYTES / 4];
   float* Ws = smem + L::W_OFF / 4;
   float* Ks = smem + L::K_OFF / 4;
   float* Us = smem + L::U_OFF / 4;
   float* Gs = smem + L::G_OFF / 4;
+  float* SSs = smem + L::SS_OFF / 4;
+  float* VDs = smem + L::VD_OFF / 4;
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // wave index as a uniform value, so that the role branches below are uniform (scalar) and the
+  // row split's barrier between them is reached by every wave, idle ones included
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int task_id = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
   if (task_id >= p.n_tasks) return;
   const Task tk = decode_task(p, order_task(p, task_id));
   const int vbase = tk.vtile * VT;
   const int hk = tk.head / p.head_ratio;
   const int g = lane >> 4, n = lane & 15;
-  const int vcol = vbase + 16 * wave + n;
+  const int cj = wave % NCW, rgrp = wave / NCW;   // column block, row group (RSF = 1: 0)
+  const int vcol = vbase + 16 * cj + n;
+  const int kt0 = KTR * rgrp;                   // first own state tile
+  // float offsets of the lane's 4-row slice of state tile kt (state staging) and of the 4-token
+  // slice of token tile tt (Vd staging)
+  auto ss_at = [&](int kt) { return (16 * cj + n) * SSP + 32 * (kt >> 1) + 8 * g + 4 * (kt & 1); };
+  auto vd_at = [&](int tt) { return (16 * cj + n) * VDP + 32 * (tt >> 1) + 8 * g + 4 * (tt & 1); };
 
   using E = float;   // element type of k/w/u/h/v_new
   const E* kb_ = (const E*)p.k + tk.b * p.sk_b + (int64_t)hk * p.sk_h;
@@ -1580,23 +1614,28 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   E* hb_ = (E*)p.h + tk.b * p.sh_b + (int64_t)tk.head * p.sh_h;
   E* vb_ = p.v_new == nullptr ? nullptr : (E*)p.v_new + tk.b * p.sv_b + (int64_t)tk.head * p.sv_h;
 
-  const bool computes = wave < NCW;   // uniform per wave
-  f32x4 S[KT];
+  const bool computes = wave < NCW * RSF;   // uniform per wave
+  f32x4 S[KTR];                             // own state tiles kt0 .. kt0 + KTR - 1
   if (computes && p.h0 != nullptr) {
     const int64_t base = (int64_t)tk.n * p.sh0_n + (int64_t)tk.head * p.sh0_h;
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt)
+    for (int i = 0; i < KTR; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        const int kt = kt0 + i;
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
-        S[kt][r] = krow >= p.K ? 0.f
-                   : p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
+        S[i][r] = krow >= p.K ? 0.f
+                  : p.h0_f32 ? ((const float*)p.h0)[off] : bf16_lo(((const unsigned short*)p.h0)[off]);
       }
   } else {
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt) S[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < KTR; ++i) S[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  if constexpr (RSF > 1)   // the state entering chunk 0, for MM1 (read after the first barrier)
+    if (computes)
+#pragma unroll
+      for (int i = 0; i < KTR; ++i) *(f32x4*)(SSs + ss_at(kt0 + i)) = S[i];
 
   // Chunk c's tiles in registers: thread i holds 16-byte pieces i, i + 256, ... of each tile
   // (rows past the sequence end and key columns past K read as zero), and wave 0 the g row.
@@ -1659,71 +1698,134 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
     }
     __syncthreads();
     if (PREFETCH && c + 1 < tk.nc) fetch(c + 1);   // in flight while chunk c is computed
-    if (!computes) continue;
-
-    // h snapshot (exact)
-    {
-      E* hdst = hb_ + (tk.boh + c) * p.sh_c;
+    if constexpr (RSF == 1) {
+      if (!computes) continue;
+      // h snapshot (exact)
+      {
+        E* hdst = hb_ + (tk.boh + c) * p.sh_c;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
+        for (int kt = 0; kt < KT; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-          if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[kt][r];
+          for (int r = 0; r < 4; ++r) {
+            const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+            if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[kt][r];
+          }
+      }
+      // MM1: acc[tt] = W S   (contraction slot g of step (kt, r) is k = pi(kt, 4g + r))
+      f32x4 acc[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          const int kcol = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
+          const f32x4 wv = *(const f32x4*)(Ws + row * WP + kcol);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[tt] = mfma_f32(wv[r], S[kt][r], acc[tt]);
         }
-    }
-    // MM1: acc[tt] = W S   (contraction slot g of step (kt, r) is k = pi(kt, 4g + r))
-    f32x4 acc[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
-        const int kcol = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
-        const f32x4 wv = *(const f32x4*)(Ws + row * WP + kcol);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[tt] = mfma_f32(wv[r], S[kt][r], acc[tt]);
       }
-    }
-    // Epilogue
-    const float a = Gs[64];
-    f32x4 Vd[4];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-        const float vn = Us[t * UP + 16 * wave + n] - acc[tt][r];
-        if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
-        Vd[tt][r] = vn * Gs[t];
-      }
-    // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r))
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt) {
-      f32x4 up = S[kt] * a;
-      const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
+      // Epilogue
+      const float a = Gs[64];
+      f32x4 Vd[4];
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-          up = mfma_f32(Ks[t * WP + krow], Vd[tt][r], up);
+          const float vn = Us[t * UP + 16 * cj + n] - acc[tt][r];
+          if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+          Vd[tt][r] = vn * Gs[t];
         }
-      S[kt] = up;
+      // MM2: S = a S + K^T Vd  (contraction slot g of step (tt, r) is token sigma(tt, 4g + r))
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        f32x4 up = S[kt] * a;
+        const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
+            up = mfma_f32(Ks[t * WP + krow], Vd[tt][r], up);
+          }
+        S[kt] = up;
+      }
+    } else {
+      float a = 0.f;
+      if (computes) {
+        a = Gs[64];
+        // h snapshot (exact), own rows
+        E* hdst = hb_ + (tk.boh + c) * p.sh_c;
+#pragma unroll
+        for (int i = 0; i < KTR; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int kt = kt0 + i;
+            const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+            if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[i][r];
+          }
+        // MM1 of own token tiles, the whole state of the column block from the staging buffer
+#pragma unroll
+        for (int q = 0; q < TPW; ++q) {
+          const int tt = TPW * rgrp + q;
+          f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+          const int row = 32 * (tt >> 1) + 8 * (n >> 2) + 4 * (tt & 1) + (n & 3);
+#pragma unroll
+          for (int kt = 0; kt < KT; ++kt) {
+            const int kcol = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1);
+            const f32x4 wv = *(const f32x4*)(Ws + row * WP + kcol);
+            const f32x4 sv = *(const f32x4*)(SSs + ss_at(kt));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc = mfma_f32(wv[r], sv[r], acc);
+          }
+          // epilogue: v_new, and Vd to the staging buffer
+          f32x4 vd;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
+            const float vn = Us[t * UP + 16 * cj + n] - acc[r];
+            if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+            vd[r] = vn * Gs[t];
+          }
+          *(f32x4*)(VDs + vd_at(tt)) = vd;
+        }
+      }
+      __syncthreads();   // Vd of all tokens staged; every MM1 read of the staged state done
+      if (computes) {
+        // MM2 of own rows: S = a S + K^T Vd, token tiles in order
+#pragma unroll
+        for (int i = 0; i < KTR; ++i) {
+          const int kt = kt0 + i;
+          f32x4 up = S[i] * a;
+          const int krow = 32 * (kt >> 1) + 8 * (n >> 2) + 4 * (kt & 1) + (n & 3);
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt) {
+            const f32x4 vdv = *(const f32x4*)(VDs + vd_at(tt));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
+              up = mfma_f32(Ks[t * WP + krow], vdv[r], up);
+            }
+          }
+          S[i] = up;
+          *(f32x4*)(SSs + ss_at(kt)) = up;   // the state entering chunk c+1 (read after the next barrier)
+        }
+      }
     }
   }
   if (computes && p.final_state != nullptr) {
     const int64_t base = (int64_t)tk.n * p.sf_n + (int64_t)tk.head * p.sf_h;
 #pragma unroll
-    for (int kt = 0; kt < KT; ++kt)
+    for (int i = 0; i < KTR; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        const int kt = kt0 + i;
         const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
         const int64_t off = base + (p.state_vk ? (int64_t)vcol * p.K + krow : (int64_t)krow * p.V + vcol);
         if (krow >= p.K) continue;
-        if (p.final_f32) ((float*)p.final_state)[off] = S[kt][r];
-        else ((__bf16*)p.final_state)[off] = (__bf16)S[kt][r];
+        if (p.final_f32) ((float*)p.final_state)[off] = S[i][r];
+        else ((__bf16*)p.final_state)[off] = (__bf16)S[i][r];
       }
   }
 }

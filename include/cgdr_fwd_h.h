@@ -95,7 +95,8 @@ typedef struct cgdr_fwd_h_tuning {
   int32_t cu_count;      /* 0: the current device's compute units; else plan for this count  */
   int32_t xcd_count;     /* 0: the current device's XCDs (accelerator complex dies)          */
   int32_t row_split;     /* 0: library's choice; 1: one compute wave per 16 value columns; 2: two,
-                            each with half of the state rows (bf16, K of 64 or 128)           */
+                            each with half of the state rows (bf16: K of 64 or 128); 4: four
+                            (fp32 inputs, K of 64 or 128; bf16 takes 2)                       */
 } cgdr_fwd_h_tuning;
 
 /* Layout of each head's block in initial_state and final_state (h is always K x V). */
@@ -190,7 +191,7 @@ typedef struct cgdr_fwd_h_plan {
   int32_t load_waves;   /* DMA waves per task workgroup (bf16 kernel)                   */
   int32_t cu_count;     /* compute units the plan was made for                          */
   int32_t xcd_count;    /* XCDs the plan was made for                                   */
-  int32_t row_split;    /* compute waves per 16 value columns (2: state rows split)        */
+  int32_t row_split;    /* compute waves per 16 value columns (2, 4: state rows split)     */
 } cgdr_fwd_h_plan;
 
 cgdr_status cgdr_fwd_h_get_plan(const cgdr_fwd_h_args* args, cgdr_fwd_h_plan* plan);

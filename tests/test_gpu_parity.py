@@ -197,6 +197,31 @@ def test_default_plan_wide_tiles_without_helpers(dev, B, T, H, K):
     _check_bf16(abi_call(dev_inputs(inp, torch.bfloat16, dev)), inp)
 
 
+@pytest.mark.parametrize("K,V,vt", [(64, 64, 16), (128, 128, 16), (32, 32, 16), (128, 128, 32), (64, 96, 32),
+                                    (48, 48, 16), (100, 100, 16)])
+def test_fp32_row_split_is_bit_identical(dev, K, V, vt):
+    """fp32 kernel with all four waves computing (each holding a share of the state rows of a
+    16-column block: row_split 4 at 16-column tiles, 2 at 32-column tiles or K = 32) against one
+    compute wave per 16 columns (row_split 1): bit-identical h, v_new and final state on a packed
+    batch with partial chunks, a length-1 sequence, grouped heads and an initial state; and the
+    exact recurrence at the fp32 tolerance (rtol 1e-4, atol 1e-5)."""
+    lens = [130, 1, 64, 200]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    inp = _case(48 + K + V, 1, int(cu[-1]), 4, K, V, Hg=2, dtype="f32", gate="linear", cu=cu)
+    d = dev_inputs(inp, torch.float32, dev)
+    want = 2 if (vt == 32 or K == 32) else 4
+    kt = torch.empty(1, int(cu[-1]), 2, K, dtype=torch.float32)
+    ut = torch.empty(1, int(cu[-1]), 4, V, dtype=torch.float32)
+    assert cgdr_amd.plan(kt, ut, cu_seqlens_len=len(cu), tuning=dict(v_tile=vt))["row_split"] == want
+    assert cgdr_amd.plan(kt, ut, cu_seqlens_len=len(cu), tuning=dict(v_tile=vt, row_split=1))["row_split"] == 1
+    base = abi_call(d, tuning=dict(v_tile=vt, row_split=1))
+    out = abi_call(d, tuning=dict(v_tile=vt))
+    for name, a, b in zip(("h", "v_new", "final"), base, out):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    for name, got, ref in zip(("h", "v_new", "final"), out, O.fwd_h(**inp, compute_dtype=np.float64)):
+        assert_close(np32(got), ref, name=name, **F32_TOL)
+
+
 def test_varlen_fp32_balanced_order(dev):
     """fp32 kernel with cu_seqlens and H % 8 == 0: the packed batch's XCD-balanced,
     longest-first dispatch order, against the exact recurrence."""
