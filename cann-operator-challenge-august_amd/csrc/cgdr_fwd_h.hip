@@ -276,8 +276,13 @@ cgdr_status make_plan(const cgdr_fwd_h_args* a, Plan* pl) {
     // Row split (two compute waves per 16 columns, each with half of the state rows): for the
     // contest numerics, whose per-element casts make the compute waves the bound.  It needs
     // an even number of 32-row state blocks (K of 64 or 128 here) and at most 8 waves.
+    // Default numerics: 16-column tiles without helpers (one short chain per CU) split too.
+    // Measured by events, row split 1 vs 2: B=2, T=2048, H=16, K=V=128, h0: 40.2 vs 37.3 us;
+    // B=2, T=4096: 62.4 vs 58.2; B=1, T=4096, H=32: 60.4 vs 58.3; B=4, T=1024, H=16: 32.6 vs
+    // 30.6.  With helpers it is slower (B=1, T=8192, H=32: 115.3 vs 125.2 us), and at 32 columns
+    // without helpers no faster (16 packed sequences of U[64, 8192], H=32: 891-895 vs 897 us).
     int rs = tu != nullptr ? tu->row_split : 0;
-    if (rs == 0) rs = pl->kernel == 2 ? 2 : 1;
+    if (rs == 0) rs = (pl->kernel == 2 || (!use_helpers && ncw == 1)) ? 2 : 1;
     if (rs == 4) rs = 2;   // the bf16 kernels split the rows two ways at most
     if (rs == 2 && !(kd == 64 || kd == 128) ) rs = 1;
     if (rs == 2 && ncw > 2) rs = 1;
