@@ -1589,8 +1589,8 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
   float* SSs = smem + L::SS_OFF / 4;
   float* VDs = smem + L::VD_OFF / 4;
 
-  // wave index as a uniform value, so that the role branches below are uniform (scalar) and the
-  // row split's barrier between them is reached by every wave, idle ones included
+  // wave index as a uniform value, so that the role branches below are scalar branches (every
+  // barrier of the chunk loop stands outside them and is reached by every wave, idle ones too)
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int task_id = xcd_remap(blockIdx.x, gridDim.x, p.n_xcd);
   if (task_id >= p.n_tasks) return;

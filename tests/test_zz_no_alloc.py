@@ -1,10 +1,10 @@
 """cgdr_fwd_h_launch_no_alloc (the entry point that allocates nothing: its workspace is a static
 per-GPU device array) against cgdr_fwd_h_launch with a caller-allocated workspace, bit for bit.
 
-Three calls in a row, each smaller than the one before, so each starts from what the last left
+Four calls in a row, each smaller than the one before, so each starts from what the last left
 in the shared scratch: token-major g (the head-major relayout of g lives in the scratch), helper
 workgroups (their progress counters), contest numerics (the per-head flags), and a head dim
-that is not a multiple of 16 (the padded copies).  The
+that is not a multiple of 16 (the padded copies), in bf16 and in fp32.  The
 oversize rejection is checked on the host, before anything touches a GPU."""
 
 import ctypes
@@ -18,10 +18,10 @@ from gpu_util import abi_call, dev_inputs
 from oracle import cgdr_oracle as O
 
 
-def _inp(seed, T, H, K=128, V=128, cu=None):
-    print(f"[no_alloc] seed={seed} T={T} H={H} K={K} V={V} varlen={cu is not None}", flush=True)
-    return O.make_inputs(seed, 1, T, H, K, V, gate="logsigmoid", gate_shift=4.0, with_h0=True, cu_seqlens=cu,
-                         profile="wy")
+def _inp(seed, T, H, K=128, V=128, cu=None, dtype="bf16"):
+    print(f"[no_alloc] seed={seed} T={T} H={H} K={K} V={V} varlen={cu is not None} {dtype}", flush=True)
+    return O.make_inputs(seed, 1, T, H, K, V, dtype=dtype, gate="logsigmoid", gate_shift=4.0, with_h0=True,
+                         cu_seqlens=cu, profile="wy")
 
 
 def _same(a, b):
@@ -37,12 +37,14 @@ def _same(a, b):
 def test_no_alloc_matches_workspace_launch(dev):
     # call 1: 8 heads x 4 V-tiles of 32 columns with helpers (progress counters), token-major g
     # (its relayout: 256 KiB of the scratch); call 2: a smaller packed batch in contest numerics
-    # call 3: K = V = 100, which runs on padded copies held in the scratch too
-    cases = [(_inp(1, 8192, 8), dict(helpers=1, v_tile=32), 0),
-             (_inp(2, 1000, 4, cu=np.array([0, 300, 301, 1000], np.int64)), None, 1),
-             (_inp(3, 300, 2, K=100, V=100), None, 0)]
-    for inp, tuning, numerics in cases:
-        d = dev_inputs(inp, torch.bfloat16, dev)
+    # call 3: K = V = 100, which runs on padded copies held in the scratch too; call 4: the same
+    # in fp32 (fp32 kernel, all four waves computing with the state rows split four ways)
+    cases = [(_inp(1, 8192, 8), dict(helpers=1, v_tile=32), 0, torch.bfloat16),
+             (_inp(2, 1000, 4, cu=np.array([0, 300, 301, 1000], np.int64)), None, 1, torch.bfloat16),
+             (_inp(3, 300, 2, K=100, V=100), None, 0, torch.bfloat16),
+             (_inp(4, 200, 2, K=100, V=100, dtype="f32"), None, 0, torch.float32)]
+    for inp, tuning, numerics, dt in cases:
+        d = dev_inputs(inp, dt, dev)
         assert d["g"].stride(1) != 1   # token-major g: the workspace holds its relayout
         ref = abi_call(d, tuning=tuning, numerics=numerics)
         got = abi_call(d, tuning=tuning, numerics=numerics, no_alloc=True)
