@@ -345,6 +345,12 @@ cgdr::FwdHParams to_params(const cgdr_fwd_h_args* a, const Plan& pl) {
   p.K = (int32_t)a->K;
   p.state_vk = a->state_layout == CGDR_STATE_VK;
   p.progress = nullptr;
+  {
+    // 16-byte stores of 4 fp32 value columns need 16-byte aligned rows of h and v_new
+    auto mult4 = [](const int64_t* st) { return st[0] % 4 == 0 && st[1] % 4 == 0 && st[2] % 4 == 0; };
+    p.vec_out = a->in_dtype == CGDR_F32 && a->V % 4 == 0 && aligned(a->h, 16) && mult4(a->stride_h) &&
+                (a->v_new == nullptr || (aligned(a->v_new, 16) && mult4(a->stride_v)));
+  }
   return p;
 }
 

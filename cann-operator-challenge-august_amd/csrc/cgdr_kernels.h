@@ -115,6 +115,8 @@ struct FwdHParams {
                         // task (kProgressStride ints; epoch-tagged, not cleared)
   int32_t* redo;        // contest: one flag per (sequence, head); a head is flagged when its flag
                         // holds this launch's epoch (flags are not cleared between launches)
+  int32_t vec_out;      // fp32 kernel: h and v_new take 16-byte stores of 4 value columns (aligned
+                        // pointers, strides and V multiples of 4 elements)
 };
 
 constexpr int kProgressStride = 32;
@@ -1752,19 +1754,24 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
         S[kt] = up;
       }
     } else {
+      // vec: h and v_new leave as 16-byte row pieces written by all 256 threads (the h snapshot
+      // from the state staging buffer, v_new from the U tile, which the epilogue overwrites
+      // with it); else each compute wave stores its own elements
+      const bool vec = p.vec_out != 0;
+      E* hdst = hb_ + (tk.boh + c) * p.sh_c;
       float a = 0.f;
       if (computes) {
         a = Gs[64];
-        // h snapshot (exact), own rows
-        E* hdst = hb_ + (tk.boh + c) * p.sh_c;
+        if (!vec) {   // h snapshot (exact), own rows
 #pragma unroll
-        for (int i = 0; i < KTR; ++i)
+          for (int i = 0; i < KTR; ++i)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int kt = kt0 + i;
-            const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
-            if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[i][r];
-          }
+            for (int r = 0; r < 4; ++r) {
+              const int kt = kt0 + i;
+              const int krow = 32 * (kt >> 1) + 8 * g + 4 * (kt & 1) + r;
+              if (krow < p.K) hdst[(int64_t)krow * p.V + vcol] = (E)S[i][r];
+            }
+        }
         // MM1 of own token tiles, the whole state of the column block from the staging buffer
 #pragma unroll
         for (int q = 0; q < TPW; ++q) {
@@ -1779,19 +1786,38 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc = mfma_f32(wv[r], sv[r], acc);
           }
-          // epilogue: v_new, and Vd to the staging buffer
+          // epilogue: v_new, and Vd to the staging buffer.  Each U element is read, and with vec
+          // overwritten by v_new, by this lane alone.
           f32x4 vd;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int t = 32 * (tt >> 1) + 8 * g + 4 * (tt & 1) + r;
-            const float vn = Us[t * UP + 16 * cj + n] - acc[r];
-            if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
+            float* up_ = Us + t * UP + 16 * cj + n;
+            const float vn = *up_ - acc[r];
+            if (vec) *up_ = vn;
+            else if (vb_ != nullptr && t < len) vb_[(t0 + t) * p.sv_t + vcol] = vn;
             vd[r] = vn * Gs[t];
           }
           *(f32x4*)(VDs + vd_at(tt)) = vd;
         }
       }
-      __syncthreads();   // Vd of all tokens staged; every MM1 read of the staged state done
+      if (vec) {
+        // h snapshot of chunk c = the state entering it, all of it in the staging buffer since
+        // the previous chunk's MM2 (rewritten only after the next barrier): thread i stores 4
+        // columns of row i / (VT / 4), then of the rows 256 / (VT / 4) further down
+        constexpr int HP = KD * VT / 4;   // 16-byte pieces of the K x Vt block
+#pragma unroll
+        for (int i = 0; i < (HP + 255) / 256; ++i) {
+          const int q = threadIdx.x + 256 * i, row = q / (VT / 4), c4 = 4 * (q % (VT / 4));
+          if (q < HP && row < p.K) {
+            f32x4 hv;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) hv[j] = SSs[(c4 + j) * SSP + row];
+            *(f32x4*)(hdst + (int64_t)row * p.V + vbase + c4) = hv;
+          }
+        }
+      }
+      __syncthreads();   // Vd and v_new of all tokens staged; every read of the staged state done
       if (computes) {
         // MM2 of own rows: S = a S + K^T Vd, token tiles in order
 #pragma unroll
@@ -1810,6 +1836,15 @@ cgdr_fwd_h_f32_kernel(const FwdHParams p) {
           }
           S[i] = up;
           *(f32x4*)(SSs + ss_at(kt)) = up;   // the state entering chunk c+1 (read after the next barrier)
+        }
+      }
+      if (vec && vb_ != nullptr) {
+        // v_new rows from the U tile (rewritten only after the next chunk's first barrier)
+        constexpr int VP = 64 * VT / 4;
+#pragma unroll
+        for (int i = 0; i < (VP + 255) / 256; ++i) {
+          const int q = threadIdx.x + 256 * i, t = q / (VT / 4), c4 = 4 * (q % (VT / 4));
+          if (q < VP && t < len) *(f32x4*)(vb_ + (t0 + t) * p.sv_t + vbase + c4) = *(const f32x4*)(Us + t * UP + c4);
         }
       }
     }

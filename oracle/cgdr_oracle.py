@@ -576,7 +576,7 @@ def make_gate(rng: np.random.Generator, B: int, T: int, H: int, kind: str = "log
     """Chunk-local cumulative log-decay ``g [B,T,H]`` (non-increasing, <= 0 in every chunk).
 
     kind="logsigmoid": cumsum of ``logsigmoid(randn + shift)`` restarted at every chunk
-    (BASELINE distributions; shift=-2 is the strongly decaying variant).
+    (the benchmark configurations' distributions; shift=-2 is the strongly decaying variant).
     kind="linear": ``g = -rate * (1..L)`` with ``rate = 0.01 + 0.0025 (h % 5)``, the mild gate of
     ``code/tests/golden/generate_golden.py:443-459``.
     """
@@ -604,10 +604,10 @@ def make_inputs(seed: int, B: int, T: int, H: int, K: int, V: int, Hg: int | Non
     """Seeded synthetic FwdH inputs.
 
     profile="baseline": k = L2-normalised randn over K; w = randn * K^-1/2; u = randn;
-        h0 = randn * h0_scale (the BASELINE distributions).  With a mild gate this w makes
+        h0 = randn * h0_scale (the benchmark configurations' distributions).  With a mild gate this w makes
         the per-chunk state transition exp(g_last) I - K^T diag(gamma) W expansive
         (spectral radius > 1), so long sequences amplify rounding differences; with the
-        BASELINE logsigmoid gate exp(g_last) ~ 1e-22 and every chunk starts afresh.
+        benchmark configurations' logsigmoid gate exp(g_last) ~ 1e-22 and every chunk starts afresh.
     profile="golden": k, u ~ U(-1,1), w ~ U(-1,1)/K, h0 ~ randn * 0.25
         (``code/tests/golden/generate_golden.py:472-490``); small w keeps the transition
         contracting.

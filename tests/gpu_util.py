@@ -29,11 +29,13 @@ _DT = {torch.bfloat16: _abi.CGDR_BF16, torch.float32: _abi.CGDR_F32}
 
 
 def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=torch.float32,
-             canary=float("nan"), tuning: dict | None = None, numerics: int = 0, no_alloc: bool = False):
+             canary=float("nan"), tuning: dict | None = None, numerics: int = 0, no_alloc: bool = False,
+             v_pad: int = 0):
     """Token-major FwdH through the C ABI into output buffers pre-filled with `canary`;
     `tuning` (fields of cgdr_fwd_h_tuning) overrides the launch plan; `numerics` is a
     cgdr_numerics; `no_alloc` calls cgdr_fwd_h_launch_no_alloc (its static scratch) instead of
-    cgdr_fwd_h_launch with a workspace."""
+    cgdr_fwd_h_launch with a workspace; `v_pad` > 0 leaves that many elements between v_new's
+    token rows (a token stride of H * V + v_pad)."""
     k, w, u, g, h0, cu = d["k"], d["w"], d["u"], d["g"], d["initial_state"], d["cu_seqlens"]
     B, T, Hg, K = k.shape
     H, V = u.shape[2], u.shape[3]
@@ -46,7 +48,10 @@ def abi_call(d: dict, save_new_value=True, output_final_state=True, final_dtype=
         NT = int(offs_h[-1])
         offs = torch.from_numpy(offs_h).to(k.device)
     h = torch.full((B, NT, H, K, V), canary, dtype=k.dtype, device=k.device)
-    v = torch.full((B, T, H, V), canary, dtype=u.dtype, device=k.device) if save_new_value else None
+    v = None
+    if save_new_value:
+        vbuf = torch.full((B, T, H * V + v_pad), canary, dtype=u.dtype, device=k.device)
+        v = vbuf.as_strided((B, T, H, V), (T * (H * V + v_pad), H * V + v_pad, V, 1))
     f = torch.full((N, H, K, V), canary, dtype=final_dtype, device=k.device) if output_final_state else None
     a = _abi.FwdHArgs()
     a.k, a.w, a.u = k.data_ptr(), w.data_ptr(), u.data_ptr()

@@ -73,15 +73,15 @@ def _three_way(out, inp, ref3):
 def _case(seed, B, T, H, K, V, Hg=None, dtype="bf16", gate="logsigmoid", shift=0.0, h0=True, cu=None,
           profile="baseline"):
     """Inputs; profile "wy" (w, u from the WY producer) is used wherever a mild gate meets long
-    sequences, since BASELINE's random w makes those transitions expansive (see
-    oracle.cgdr_oracle.make_inputs)."""
+    sequences, since the benchmark distributions' random w makes those transitions expansive
+    (oracle.cgdr_oracle.make_inputs)."""
     print(f"[case] seed={seed} B={B} T={T} H={H} Hg={Hg} K={K} V={V} dtype={dtype} gate={gate} "
           f"shift={shift} h0={h0} varlen={cu is not None} profile={profile}", flush=True)
     return O.make_inputs(seed, B, T, H, K, V, Hg=Hg, dtype=dtype, gate=gate, gate_shift=shift,
                          with_h0=h0, cu_seqlens=cu, profile=profile)
 
 
-# ---------------------------------------------------------------- BASELINE configurations
+# ---------------------------------------------------------------- benchmark configurations
 
 @pytest.mark.parametrize("gate", ["logsigmoid", "linear"])
 def test_config0_fp32(dev, gate):
@@ -115,7 +115,7 @@ def test_config4_wide_value_strong_decay(dev):
 
 def test_config3_varlen_full_size(dev):
     """Config 3 at its full size: 16 sequences of seeded lengths in [64, 8192] (none a multiple
-    of 64), H=32, K=V=128, per-sequence h0, BASELINE's distributions.  All heads against the
+    of 64), H=32, K=V=128, per-sequence h0, the benchmark distributions.  All heads against the
     bf16 rounding model elementwise (rtol=2e-2, atol=2e-3); every fourth head against the exact
     recurrence within 1% of the tensor's scale."""
     cu = O.varlen_cu_seqlens(3, 16, 64, 8192)
@@ -220,6 +220,20 @@ def test_fp32_row_split_is_bit_identical(dev, K, V, vt):
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
     for name, got, ref in zip(("h", "v_new", "final"), out, O.fwd_h(**inp, compute_dtype=np.float64)):
         assert_close(np32(got), ref, name=name, **F32_TOL)
+
+
+def test_fp32_unaligned_v_new_stride(dev):
+    """fp32 kernel with a v_new token stride of H * V + 2 elements (8-byte but not 16-byte aligned
+    rows): the compute waves store h and v_new element by element instead of the workgroup's
+    16-byte row pieces; the results equal the aligned call's bit for bit, at every row split."""
+    inp = _case(77, 2, 200, 4, 64, 64, dtype="f32", gate="linear")
+    d = dev_inputs(inp, torch.float32, dev)
+    for rs in (1, 2, 4):
+        base = abi_call(d, tuning=dict(row_split=rs))
+        out = abi_call(d, tuning=dict(row_split=rs), v_pad=2)
+        assert out[1].stride(1) == 4 * 64 + 2
+        for name, a, b in zip(("h", "v_new", "final"), base, out):
+            assert torch.equal(a.view(torch.int32), b.contiguous().view(torch.int32)), (rs, name)
 
 
 def test_varlen_fp32_balanced_order(dev):
