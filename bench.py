@@ -258,21 +258,34 @@ def progress(msg: str) -> None:
 
 
 def time_steps(torch, dev, step, steps, warmup):
+    """`warmup` untimed steps, then exactly `steps` steps between two synchronisations.  One
+    pair of HIP events on the launch stream brackets the timed steps (events around every step
+    would add a ~7 us gap to each).  Returns the wall time, the events' time per step (the
+    average launch duration while the host keeps the stream fed, else an upper bound of it) and
+    the host's issue time per step."""
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         step()
-        ends[i].record(stream)
+    e1.record(stream)
+    issue = time.perf_counter() - t0
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall, e0.elapsed_time(e1) / steps, issue * 1e3 / steps
+
+
+def timing_fields(avg_ms, host_ms):
+    """kernel_ms is the events' time per step; launch_bound marks runs where the host's issue
+    time per step comes within 10 % of it (then the GPU idled between launches, and kernel_ms
+    overstates the launch duration)."""
+    return {"kernel_ms": avg_ms, "host_ms_per_step": host_ms, "launch_bound": host_ms > 0.9 * avg_ms}
 
 
 def wy_bytes(B, T, H, Hg, K, V, s=2):
@@ -321,9 +334,8 @@ def main_wy(args, torch, cgdr_amd, dev, forward: bool):
         step = lambda: cgdr_amd.wy_fwd(k, v, beta, g=a)
         nbytes = wy_bytes(B, T, H, Hg, K, V)
         name, tfile = "wy", os.path.join(ROOT, "profiles", "cgdr_wy_bf16_T32768_H32_hbm_traffic.md")
-    wall, kern_ms = time_steps(torch, dev, step, args.steps, args.warmup)
+    wall, avg_ms, host_ms = time_steps(torch, dev, step, args.steps, args.warmup)
     progress(f"timed {args.steps} {name} steps")
-    avg_ms = sum(kern_ms) / len(kern_ms)
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
     traffic = None
     if tfile and os.path.exists(tfile):
@@ -347,8 +359,7 @@ def main_wy(args, torch, cgdr_amd, dev, forward: bool):
         "data": "synthetic",
         "config": {"workload": what + ", long-context prefill", **W, "parallelism": "none (1 GPU)"},
         "hbm_gbps": achieved,
-        "kernel_ms": avg_ms,
-        "kernel_ms_min": min(kern_ms),
+        **timing_fields(avg_ms, host_ms),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic, "algorithmic_bytes": nbytes},
     }
@@ -365,9 +376,9 @@ def main_chunk_o(args, torch, cgdr_amd, dev):
     q, k, v, h, g = make_chunk_o_inputs(torch, dev, B, T, H, Hg, K, V)
     torch.cuda.synchronize()
     progress("chunk_o inputs resident in HBM")
-    wall, kern_ms = time_steps(torch, dev, lambda: cgdr_amd.chunk_fwd_o(q, k, v, h, g=g), args.steps, args.warmup)
+    wall, avg_ms, host_ms = time_steps(torch, dev, lambda: cgdr_amd.chunk_fwd_o(q, k, v, h, g=g), args.steps,
+                                       args.warmup)
     progress(f"timed {args.steps} chunk_o steps")
-    avg_ms = sum(kern_ms) / len(kern_ms)
     nbytes = chunk_o_bytes(B, T, H, Hg, K, V, NT)
     flops = chunk_o_flops(B, NT, H, K, V)
     achieved = nbytes / (avg_ms * 1e-3) / 1e9
@@ -393,8 +404,7 @@ def main_chunk_o(args, torch, cgdr_amd, dev):
         "config": {"workload": "chunk output o from FwdH's h and v_new, long-context prefill", **W,
                    "parallelism": "none (1 GPU)"},
         "hbm_gbps": achieved,
-        "kernel_ms": avg_ms,
-        "kernel_ms_min": min(kern_ms),
+        **timing_fields(avg_ms, host_ms),
         "tflops": flops / (avg_ms * 1e-3) / 1e12,
         "plan": cgdr_amd.chunk_o.plan(q, v),
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -475,24 +485,9 @@ def main():
         return cgdr_amd.chunk_gated_delta_rule_fwd_h(k, w, u, g=g, initial_state=h0, output_final_state=True,
                                                      cu_seqlens=cu, numerics=args.numerics, tuning=tuning)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream(dev)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    avg_ms = sum(kern_ms) / len(kern_ms)
-    progress(f"timed {args.steps} fwd_h steps; per-step ms: " + " ".join(f"{x:.4f}" for x in kern_ms))
+    wall, avg_ms, host_ms = time_steps(torch, dev, step, args.steps, args.warmup)
+    progress(f"timed {args.steps} fwd_h steps: {avg_ms * 1e3:.1f} us per step by events, "
+             f"{host_ms * 1e3:.1f} us host issue time per step")
 
     es = k.element_size()
     nbytes = algorithmic_bytes(B, T, H, Hg, K, V, NT, N, s_in=es, s_out=es, h0_bytes=4 if h0 is not None else 0)
@@ -528,8 +523,7 @@ def main():
                    "numerics": args.numerics, "parallelism": "none (1 GPU)",
                    **({"tuning": tuning} if tuning else {})},
         "hbm_gbps": achieved,
-        "kernel_ms": avg_ms,
-        "kernel_ms_min": min(kern_ms),
+        **timing_fields(avg_ms, host_ms),
         "tflops": flops / (avg_ms * 1e-3) / 1e12,
         "mfma_util": flops / (avg_ms * 1e-3) / 1e12 / (F32_MFMA_PEAK_TFLOPS if es == 4 else BF16_MFMA_PEAK_TFLOPS),
         "plan": plan,
