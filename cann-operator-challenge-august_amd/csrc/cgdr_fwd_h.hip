@@ -118,18 +118,38 @@ bool aligned(const void* p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes
 
 // Compute units and XCDs of the calling thread's current device (tuning overrides first; the
 // MI355X figures when no device answers, e.g. when planning on a host without a GPU).
+// The counts are queried once per device and kept (they cannot change while the process runs;
+// every call plans twice, for its workspace size and for its launch).
+constexpr int kTopoDevices = 64;
+std::atomic<int> g_topo_cus[kTopoDevices], g_topo_xcds[kTopoDevices];
+
 void topology(const cgdr_fwd_h_tuning* tu, int* cus, int* xcds) {
   *cus = kDefaultCUs;
   *xcds = kDefaultXCDs;
-  int dev = 0, v = 0;
-  const bool have_dev = hipGetDevice(&dev) == hipSuccess;
+  int dev = 0, c = 0, x = 0;
+  if (hipGetDevice(&dev) == hipSuccess) {
+    const bool cached = dev >= 0 && dev < kTopoDevices;
+    if (cached) {
+      c = g_topo_cus[dev].load(std::memory_order_relaxed);
+      x = g_topo_xcds[dev].load(std::memory_order_relaxed);
+    }
+    if (c <= 0 || x <= 0) {
+      int v = 0;
+      if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) c = v;
+      if (hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0) x = v;
+      (void)hipGetLastError();   // a failed query is not the caller's error
+      if (cached && c > 0 && x > 0) {
+        g_topo_cus[dev].store(c, std::memory_order_relaxed);
+        g_topo_xcds[dev].store(x, std::memory_order_relaxed);
+      }
+    }
+  } else {
+    (void)hipGetLastError();   // no device on this host (planning only): not the caller's error
+  }
+  if (c > 0) *cus = c;
+  if (x > 0) *xcds = x;
   if (tu != nullptr && tu->cu_count > 0) *cus = tu->cu_count;
-  else if (have_dev && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-    *cus = v;
   if (tu != nullptr && tu->xcd_count > 0) *xcds = tu->xcd_count;
-  else if (have_dev && hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0)
-    *xcds = v;
-  (void)hipGetLastError();   // a failed query on a host without a GPU is not the caller's error
 }
 
 cgdr_status check_tuning(const cgdr_fwd_h_tuning* tu) {

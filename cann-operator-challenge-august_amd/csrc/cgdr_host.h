@@ -3,6 +3,7 @@
 // reference's host code).
 #pragma once
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -24,15 +25,26 @@ inline cgdr_status fail(cgdr_status st, const char* fmt, ...) {
 }
 
 // XCDs of the calling thread's current device, which the hardware deals workgroups to
-// round-robin (8 on MI355X, the figure used when no device answers).
+// round-robin (8 on MI355X, the figure used when no device answers).  Queried once per device
+// and kept: the count cannot change while the process runs.
 inline int device_xcds() {
-  int dev = 0, v = 0;
-  int n = 8;
-  if (hipGetDevice(&dev) == hipSuccess &&
-      hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0)
-    n = v;
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 8;
+  }
+  const bool cached = dev >= 0 && dev < 64;
+  if (cached) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int v = 0;
+  const bool ok = hipDeviceGetAttribute(&v, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && v > 0;
   (void)hipGetLastError();
-  return n;
+  if (!ok) return 8;
+  if (cached) cache[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 }  // namespace cgdr_host
