@@ -251,6 +251,37 @@ def test_plan_headline_fills_the_chip(lib):
     assert p.v_tile == 16 and p.workgroups == 16 * 8
 
 
+@pytest.mark.parametrize("B,T,H,K,V,vt,rs", [
+    (2, 2048, 16, 128, 128, 16, 4),    # 256 tasks of 16 columns: one round, all waves on rows
+    (4, 4096, 32, 128, 128, 64, 1),    # 1,024 / 512 / 256 tasks: one round of 64 columns wins
+    (4, 2048, 64, 128, 128, 64, 1),
+    (3, 2048, 16, 128, 128, 32, 2),    # 384 tasks of 16 columns = 2 rounds; 192 of 32 = 1
+    (2, 2048, 16, 256, 256, 32, 1),    # K = 256: no row split, 32 columns fill one round
+    (1, 256, 2, 64, 64, 16, 4),        # the CPU-runnable case: 8 tasks, all four waves on rows
+    (2, 2048, 16, 32, 32, 16, 2),      # K = 32: two 16-row tiles, split two ways at most
+])
+def test_plan_fp32_tile_width_and_row_split(lib, B, T, H, K, V, vt, rs):
+    """fp32 plans: the tile width with the least (rounds of the device) x (relative time of one
+    round: 1 / 1.62 / 2.25 at 16 / 32 / 64 columns with the row split, 1 / 1.13 / 1.22 at
+    K = 256), and the row split that puts all four waves on state rows where K <= 128."""
+    p = _abi.get_plan(_mi355x(_args(B=B, T=T, H=H, Hg=H, K=K, V=V, dtype=_abi.CGDR_F32)))
+    assert (p.kernel, p.v_tile, p.row_split) == (1, vt, rs)
+    assert p.workgroups == B * H * (V // vt) and p.lds_bytes <= 160 * 1024
+
+
+def test_plan_bf16_row_split_default(lib):
+    """bf16, default numerics: the state rows are split two ways at 16-column tiles without
+    helpers (short sequences), not in helper mode (the headline) nor at 32-column tiles."""
+    p = _abi.get_plan(_mi355x(_args(B=2, T=2048, H=16, Hg=16, K=128, V=128)))
+    assert (p.v_tile, p.helpers, p.row_split) == (16, 0, 2)
+    p = _abi.get_plan(_mi355x(_args(B=1, T=32768, H=32, Hg=32, K=128, V=128)))
+    assert (p.v_tile, p.helpers, p.row_split) == (32, 1, 1)
+    p = _abi.get_plan(_mi355x(_args(B=4, T=8192, H=8, Hg=8, K=128, V=256)))
+    assert (p.v_tile, p.helpers, p.row_split) == (32, 0, 1)
+    p = _abi.get_plan(_mi355x(_args(B=2, T=2048, H=16, Hg=16, K=32, V=32)))
+    assert p.row_split == 1        # the bf16 split needs K of 64 or 128
+
+
 def test_plan_follows_the_device_topology(lib):
     """The plan is made for the device's CU and XCD counts: on a smaller device (a partition
     of 64 CUs in 2 XCDs) the headline's 128 tasks + 128 helpers no longer fit, so it runs
