@@ -222,6 +222,35 @@ def test_fp32_row_split_is_bit_identical(dev, K, V, vt):
         assert_close(np32(got), ref, name=name, **F32_TOL)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_fp32_random_shapes(dev, seed):
+    """fp32 kernel on seeded random shapes: K and V from 32 to 256 (multiples of 16 and not),
+    grouped heads, fixed-length or packed batches with ragged lengths, with or without h0,
+    either gate; the default plan against the exact recurrence
+    (rtol 1e-4, atol 1e-5) and, bit for bit, against one compute wave per 16 columns."""
+    rng = np.random.default_rng(9000 + seed)
+    K = int(rng.choice([32, 48, 64, 96, 100, 128, 160, 256]))
+    V = int(rng.choice([32, 48, 64, 80, 96, 128]))
+    Hg = int(rng.choice([1, 2]))
+    H = Hg * int(rng.choice([1, 2, 4]))
+    gate = str(rng.choice(["linear", "logsigmoid"]))
+    h0 = bool(rng.integers(2))
+    if rng.integers(2):
+        lens = [int(x) for x in rng.integers(1, 260, size=int(rng.integers(1, 5)))]
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        B, T = 1, int(cu[-1])
+    else:
+        cu, B, T = None, int(rng.integers(1, 3)), int(rng.integers(1, 300))
+    inp = _case(9000 + seed, B, T, H, K, V, Hg=Hg, dtype="f32", gate=gate, h0=h0, cu=cu)
+    d = dev_inputs(inp, torch.float32, dev)
+    out = abi_call(d)
+    base = abi_call(d, tuning=dict(row_split=1))
+    for name, a, b in zip(("h", "v_new", "final"), base, out):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    for name, got, ref in zip(("h", "v_new", "final"), out, O.fwd_h(**inp, compute_dtype=np.float64)):
+        assert_close(np32(got), ref, name=name, **F32_TOL)
+
+
 def test_fp32_unaligned_v_new_stride(dev):
     """fp32 kernel with a v_new token stride of H * V + 2 elements (8-byte but not 16-byte aligned
     rows): the compute waves store h and v_new element by element instead of the workgroup's
