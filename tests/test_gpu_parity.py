@@ -251,6 +251,38 @@ def test_fp32_random_shapes(dev, seed):
         assert_close(np32(got), ref, name=name, **F32_TOL)
 
 
+@pytest.mark.parametrize("seed", range(10))
+def test_bf16_random_shapes(dev, seed):
+    """bf16 kernel, default numerics, on seeded random shapes (K and V from 32 to 256,
+    multiples of 16 and not; grouped heads; fixed-length or packed ragged batches; h0 or
+    none): the default plan against the bf16 rounding model elementwise (rtol 2e-2, atol
+    2e-3) and the exact recurrence within 1 % of scale, and bit for bit against other plans
+    (16-column tiles without helpers and without the row split; 32-column tiles with
+    helpers)."""
+    rng = np.random.default_rng(9500 + seed)
+    K = int(rng.choice([32, 48, 64, 96, 100, 128, 160, 256]))
+    V = int(rng.choice([32, 64, 96, 128, 256]))
+    Hg = int(rng.choice([1, 2]))
+    H = Hg * int(rng.choice([1, 2, 4]))
+    h0 = bool(rng.integers(2))
+    if rng.integers(2):
+        lens = [int(x) for x in rng.integers(1, 300, size=int(rng.integers(1, 5)))]
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+        B, T = 1, int(cu[-1])
+    else:
+        cu, B, T = None, int(rng.integers(1, 3)), int(rng.integers(1, 400))
+    inp = _case(9500 + seed, B, T, H, K, V, Hg=Hg, gate="logsigmoid", h0=h0, cu=cu)
+    d = dev_inputs(inp, torch.bfloat16, dev)
+    out = abi_call(d)
+    _check_bf16(out, inp)
+    for tu in (dict(v_tile=16, helpers=0, row_split=1), dict(v_tile=32, helpers=1)):
+        if V % tu["v_tile"]:
+            continue
+        for name, a, b in zip(("h", "v_new", "final"), out, abi_call(d, tuning=tu)):
+            assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a.view(torch.int32),
+                               b.view(torch.int16) if b.dtype == torch.bfloat16 else b.view(torch.int32)), (tu, name)
+
+
 def test_fp32_unaligned_v_new_stride(dev):
     """fp32 kernel with a v_new token stride of H * V + 2 elements (8-byte but not 16-byte aligned
     rows): the compute waves store h and v_new element by element instead of the workgroup's
